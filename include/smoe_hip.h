@@ -1,0 +1,259 @@
+/*
+ * smoe_hip.h -- C ABI of the MI355X (gfx950) MoE compute backend.
+ *
+ * Drop-in for the FFN part of S-MoE's compute-backend boundary
+ * (src/compute/metal_bridge.h in the reference).  Two layers of entry points:
+ *
+ *  1. The reference's own surface, same names, same argument meaning, same
+ *     handle/wait contract (smoe_metal_*).  A caller that linked the Metal
+ *     bridge links this library instead.  One difference is forced by the
+ *     hardware: expert pointers (packed_*, scales_*) must be device addresses
+ *     (HBM-resident expert pool, hipMalloc'd) or hipHostMalloc'd pinned
+ *     memory -- the reference wraps unified-memory host pages instead.
+ *     Activations stay host pointers, copied in and out as the reference
+ *     copies them (metal_bridge.mm:466, :440, :643-644).
+ *
+ *  2. Device-resident entry points (smoe_hip_*): the whole MoE block of one
+ *     layer (RMSNorm, router GEMV, softmax + top-k, fused Q4 expert FFN,
+ *     rank-weighted combine, residual) on device pointers, asynchronous on
+ *     the context's stream, no host round trip, capturable in a HIP graph.
+ *     They return an int status (SMOE_OK or a negative SMOE_ERR_*).
+ *
+ * All pointers are plain C pointers, all sizes plain integers.  One context
+ * is driven by one host thread (the reference's threading contract,
+ * metal_bridge.mm:97).
+ */
+#ifndef SMOE_HIP_H
+#define SMOE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes of the smoe_hip_* entry points */
+#define SMOE_OK            0
+#define SMOE_ERR_ARG      -1   /* NULL pointer or zero-sized argument */
+#define SMOE_ERR_SHAPE    -2   /* dims not multiples of the group size, k too large, ... */
+#define SMOE_ERR_BITS     -3   /* bits != 4 (only SMOE-Q4 is implemented) */
+#define SMOE_ERR_HIP      -4   /* a HIP runtime call failed (see smoe_hip_last_error) */
+#define SMOE_ERR_CAPACITY -5   /* scratch reserved by smoe_hip_reserve is too small */
+#define SMOE_ERR_CAPTURE  -6   /* would allocate while the stream is being captured */
+
+/* limits (reference: scout.hpp:32 MAX_ACTIVE, metal_bridge.h:134-135) */
+#define SMOE_MAX_ACTIVE        16
+#define SMOE_MAX_EXPERTS      512
+#define SMOE_MAX_DIM         8192
+#define SMOE_MAX_FFN_BATCH     64
+#define SMOE_MAX_FFN_BATCH_DIM 16384
+
+/* Opaque execution context (reference: metal_bridge.h:35). */
+typedef struct SmoeMetalCtx SmoeMetalCtx;
+
+/* ======================================================================== */
+/* 1. Reference surface (metal_bridge.h)                                     */
+/* ======================================================================== */
+
+/* metal_bridge.h:47 -- select device 0 (or the current device), create a
+ * stream, allocate the per-slot scratch sized by slot_bytes.  NULL on failure
+ * (no GPU, allocation failure). */
+SmoeMetalCtx* smoe_metal_init(size_t slot_bytes);
+
+/* metal_bridge.h:50 -- release everything; NULL-safe. */
+void smoe_metal_destroy(SmoeMetalCtx* ctx);
+
+/* metal_bridge.h:74-90 -- one expert: gate+up+SiLU, then down, into the
+ * context's scratch region `expert_index`.  hidden_vec and output_vec are
+ * accepted for signature compatibility and not written (as in the reference,
+ * metal_bridge.mm:304-432): fetch the result with smoe_metal_wait.  Returns a
+ * handle, or NULL on invalid arguments. */
+void* smoe_metal_fused_ffn(SmoeMetalCtx* ctx,
+                           const uint8_t* packed_gate, const uint16_t* scales_gate,
+                           const uint8_t* packed_up, const uint16_t* scales_up,
+                           const uint8_t* packed_down, const uint16_t* scales_down,
+                           const float* input_vec, float* hidden_vec, float* output_vec,
+                           uint32_t gate_rows, uint32_t gate_cols,
+                           uint32_t down_rows, uint32_t down_cols,
+                           uint32_t group_size, uint32_t bits, uint32_t expert_index);
+
+/* metal_bridge.h:92 -- wait for `handle`, copy `cols` floats of scratch region
+ * `expert_index` into output_vec (host).  NULL ctx or handle: no-op. */
+void smoe_metal_wait(SmoeMetalCtx* ctx, void* handle, float* output_vec,
+                     uint32_t expert_index, uint32_t cols);
+
+/* metal_bridge.h:106-114 */
+typedef struct {
+    const uint8_t*  packed_gate;
+    const uint16_t* scales_gate;
+    const uint8_t*  packed_up;
+    const uint16_t* scales_up;
+    const uint8_t*  packed_down;
+    const uint16_t* scales_down;
+    uint32_t        slot;
+} SmoeExpertBlob;
+
+/* metal_bridge.h:116-125 -- n same-shaped experts on one input vector, all
+ * gate/up work then all down work, one handle for the group; each expert's
+ * result lands in scratch region experts[i].slot.  NULL if n_experts is 0 or
+ * above SMOE_MAX_ACTIVE, or a slot is out of range. */
+void* smoe_metal_fused_ffn_group(SmoeMetalCtx* ctx, const SmoeExpertBlob* experts,
+                                 uint32_t n_experts, const float* input_vec,
+                                 uint32_t gate_rows, uint32_t gate_cols,
+                                 uint32_t down_rows, uint32_t down_cols,
+                                 uint32_t group_size, uint32_t bits);
+
+/* metal_bridge.h:137-151 -- one expert applied to `batch` token rows
+ * (input_mat row-major [batch x gate_cols]).  NULL when batch is 0 or above
+ * SMOE_MAX_FFN_BATCH or a dim exceeds SMOE_MAX_FFN_BATCH_DIM (the caller falls
+ * back to the per-token path, prefill.cpp:386-405). */
+void* smoe_metal_fused_ffn_batch(SmoeMetalCtx* ctx,
+                                 const uint8_t* packed_gate, const uint16_t* scales_gate,
+                                 const uint8_t* packed_up, const uint16_t* scales_up,
+                                 const uint8_t* packed_down, const uint16_t* scales_down,
+                                 const float* input_mat, uint32_t batch,
+                                 uint32_t gate_rows, uint32_t gate_cols,
+                                 uint32_t down_rows, uint32_t down_cols,
+                                 uint32_t group_size, uint32_t bits);
+
+/* metal_bridge.h:153-154 -- wait, copy out_mat [batch x cols] (host). */
+void smoe_metal_wait_ffn_batch(SmoeMetalCtx* ctx, void* handle, float* out_mat,
+                               uint32_t batch, uint32_t cols);
+
+/* metal_bridge.h:221 -- the reference wraps host pages for the GPU.  Here it
+ * records the range when it is device or pinned memory the GPU can read, and
+ * warns on stderr otherwise (host pages cannot be mapped after the fact). */
+void smoe_metal_register_buffer(SmoeMetalCtx* ctx, const void* ptr, size_t size_in_bytes);
+
+/* metal_bridge.h:224 -- number of expert-FFN kernel dispatches submitted. */
+uint64_t smoe_metal_kernel_dispatches(const SmoeMetalCtx* ctx);
+
+/* ======================================================================== */
+/* 2. Device-resident MoE block (MI355X path)                                */
+/* ======================================================================== */
+
+/* Shape of one MoE layer (reference: SmoeModelConfig, common.hpp:118-142). */
+typedef struct {
+    uint32_t d_model;     /* hidden size D            (2048 / 4096) */
+    uint32_t n_experts;   /* experts per layer E      (128)         */
+    uint32_t top_k;       /* routed experts per token (8), <= 16    */
+    uint32_t d_ff;        /* expert intermediate I    (768 / 1536)  */
+    uint32_t group_size;  /* SMOE quant group         (64)          */
+    uint32_t bits;        /* must be 4                              */
+    uint32_t norm_topk;   /* renormalise the k weights (Qwen3: 1)   */
+} SmoeMoeShape;
+
+/* Weights of one MoE layer, all device pointers.  Expert e's blob starts at
+ * experts + e * expert_stride and holds the six tensors at the offsets of the
+ * vault's TensorDescriptors (ExpertLayout, prefill.hpp:38-53;
+ * build_expert_blob, shatter_moe.py:627-674). */
+typedef struct {
+    const uint16_t* norm_w;     /* [d_model] bf16 post-attention norm weight */
+    const uint16_t* router_w;   /* [n_experts x d_model] bf16 (mlp.gate.weight) */
+    const uint8_t*  experts;    /* blob of expert 0 of this layer */
+    uint64_t        expert_stride;
+    uint64_t gate_packed_offset, gate_scales_offset;
+    uint64_t up_packed_offset,   up_scales_offset;
+    uint64_t down_packed_offset, down_scales_offset;
+} SmoeMoeLayer;
+
+/* Use `hip_stream` (a hipStream_t) for all later work of this context; NULL
+ * selects the context's own stream.  No synchronisation is implied. */
+int smoe_hip_set_stream(SmoeMetalCtx* ctx, void* hip_stream);
+
+/* Synchronise the context's stream. */
+int smoe_hip_synchronize(SmoeMetalCtx* ctx);
+
+/* Reserve device scratch for layers of this shape and up to max_tokens tokens
+ * per call.  Entry points reserve on demand when the stream is not being
+ * captured; under graph capture they fail with SMOE_ERR_CAPTURE instead. */
+int smoe_hip_reserve(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, uint32_t max_tokens);
+
+/* Decode MoE block (decode.cpp:236-509): for each of n_tokens rows of hidden
+ * [n_tokens x d_model] (device, updated in place):
+ *   normed = rms_norm_bf16(hidden, norm_w)          common.hpp:245-256
+ *   logits = router_w . normed                      common.hpp:293-306
+ *   ids, w = top_k(softmax(logits)), renormalised   scout.cpp:77-123, decode.cpp:290-302
+ *   hidden += sum_r w_r * FFN_{ids_r}(normed)       kernels.metal:308-365, decode.cpp:482-509
+ * ids_out [n_tokens x top_k] and weights_out [n_tokens x top_k] are optional
+ * device pointers.  Asynchronous on the context stream. */
+int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
+                        const SmoeMoeLayer* layer, float* hidden, uint32_t n_tokens,
+                        uint32_t* ids_out, float* weights_out);
+
+/* Prefill MoE block (prefill.cpp:308-453) over n_tokens rows: the same math
+ * with the layer-major expert grouping (permute by expert, grouped GEMM,
+ * weighted scatter).  Optional device outputs of the permute:
+ *   expert_offsets [n_experts+1], sorted_tokens [n_tokens*top_k],
+ *   union_ids [n_experts] (first-appearance order, prefill.cpp:55-68),
+ *   union_size [1]. */
+int smoe_hip_moe_prefill(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
+                         const SmoeMoeLayer* layer, float* hidden, uint32_t n_tokens,
+                         uint32_t* ids_out, float* weights_out,
+                         uint32_t* expert_offsets, uint32_t* sorted_tokens,
+                         uint32_t* union_ids, uint32_t* union_size);
+
+/* Scout::compute_top_k (scout.cpp:718-720 -> top_k :77-123) on device:
+ * scores [n_rows x n] -> ids [n_rows x k], weights [n_rows x k]. */
+int smoe_hip_compute_top_k(SmoeMetalCtx* ctx, const float* scores, uint32_t n_rows,
+                           uint32_t n, uint32_t k, uint32_t* ids, float* weights,
+                           int norm_topk);
+
+/* Token-by-expert permute (prefill.cpp:38-68, :315-332) of ids [n_tokens x
+ * top_k] on device: stable counting sort of (token, rank) pairs by expert.
+ * expert_offsets [n_experts+1]; sorted_tokens / sorted_weights [n_tokens*top_k]
+ * (ascending token order inside each expert); union_ids [n_experts] in order
+ * of first appearance; union_size [1]. */
+int smoe_hip_permute(SmoeMetalCtx* ctx, const uint32_t* ids, const float* weights,
+                     uint32_t n_tokens, uint32_t top_k, uint32_t n_experts,
+                     uint32_t* expert_offsets, uint32_t* sorted_tokens,
+                     float* sorted_weights, uint32_t* union_ids, uint32_t* union_size);
+
+/* quantize_smoeq4 (shatter_moe.py:331-368) on device: w [n] fp32 ->
+ * packed [n/2] (low nibble = even index), scales [n/group_size] fp16 bits.
+ * n must be a multiple of group_size. */
+int smoe_hip_quantize_q4(SmoeMetalCtx* ctx, const float* w, uint64_t n,
+                         uint32_t group_size, uint8_t* packed, uint16_t* scales);
+
+/* ---- synthetic inputs (counter-based RNG, reproducible on the host) ----- */
+/* out[i] = stddev * N(0,1)(key(seed, stream), i) */
+int smoe_hip_synth_normal(SmoeMetalCtx* ctx, float* out, uint64_t n, uint64_t seed,
+                          uint64_t stream, float stddev);
+/* bf16 round-to-nearest-even of the same draw */
+int smoe_hip_synth_bf16(SmoeMetalCtx* ctx, uint16_t* out, uint64_t n, uint64_t seed,
+                        uint64_t stream, float stddev);
+/* n_layers x n_experts expert blobs at base + (l*n_experts + e)*expert_stride:
+ * each of gate [d_ff x d_model], up, down [d_model x d_ff] drawn
+ * N(0, stddev) from stream (first_layer+l)<<32 | e<<4 | m (m = 0 gate, 1 up,
+ * 2 down) and quantized to SMOE-Q4 in the build_expert_blob layout. */
+int smoe_hip_synth_expert_pool(SmoeMetalCtx* ctx, uint8_t* base, uint32_t first_layer,
+                               uint32_t n_layers, uint32_t n_experts,
+                               uint64_t expert_stride, const SmoeMoeShape* shape,
+                               uint64_t seed, float stddev);
+
+/* ---- per-kernel timing (telemetry; cf. the reference's --instrument buckets,
+ * decode.hpp:36-74, and smoe_metal_kernel_dispatches) ------------------------
+ * When enabled, every kernel the context launches outside graph capture is
+ * bracketed by HIP events on the stream it runs on; profile_read returns the
+ * launch count and summed event time of one kernel kind. */
+#define SMOE_KERNEL_ROUTE         0   /* RMSNorm + router GEMV + top-k        */
+#define SMOE_KERNEL_GATE_UP       1   /* gate/up GEMV + SiLU, all k experts   */
+#define SMOE_KERNEL_DOWN_COMBINE  2   /* down GEMV + weighted combine + residual */
+#define SMOE_KERNEL_DOWN_SLOTS    3   /* down GEMV, per-slot outputs          */
+#define SMOE_KERNEL_TOPK          4
+#define SMOE_KERNEL_PERMUTE       5
+#define SMOE_KERNEL_GROUPED_GATE_UP 6
+#define SMOE_KERNEL_GROUPED_DOWN  7
+#define SMOE_KERNEL_SCATTER       8
+#define SMOE_KERNEL_KINDS        16
+int smoe_hip_profile_enable(SmoeMetalCtx* ctx, int enable);
+int smoe_hip_profile_read(SmoeMetalCtx* ctx, uint32_t kernel, uint64_t* launches, double* total_ms);
+
+/* last HIP error string seen by this context ("" if none) */
+const char* smoe_hip_last_error(const SmoeMetalCtx* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SMOE_HIP_H */

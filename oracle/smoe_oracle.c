@@ -1,0 +1,510 @@
+/*
+ * smoe_oracle.c -- CPU restatement of S-MoE's MoE block (see smoe_oracle.h).
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP path and the timed CPU
+ * baseline.  Build with -ffp-contract=off so that every a*b+c below is two
+ * roundings, as in the reference's scalar x86 build of src/common.hpp and
+ * src/scout/scout.cpp; the generator uses explicit fmaf only.
+ */
+#include "smoe_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ------------------------------------------------------------------------ */
+/* number formats                                                            */
+/* ------------------------------------------------------------------------ */
+
+/* src/common.hpp:238-243: bf16 -> f32 is the 16-bit left shift */
+float orc_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+uint16_t orc_f32_to_bf16(float f)
+{
+    uint32_t x = f2u(f);
+    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((x >> 16) | 0x40u);
+    x += 0x7FFFu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+
+float orc_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = ((uint32_t)h >> 10) & 0x1Fu;
+    uint32_t m = (uint32_t)h & 0x3FFu;
+    if (e == 0) {
+        if (m == 0) return u2f(sign);
+        float v = (float)m * 5.9604644775390625e-8f;   /* m * 2^-24, exact */
+        return u2f(f2u(v) | sign);
+    }
+    if (e == 31) return u2f(sign | 0x7F800000u | (m << 13));
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* IEEE binary16 round-to-nearest-even, the cast numpy's astype(float16)
+ * performs in scripts/shatter_moe.py:354 */
+uint16_t orc_f32_to_f16(float f)
+{
+    uint32_t x = f2u(f);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t a = x & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) {                       /* inf / nan */
+        if (a == 0x7F800000u) return (uint16_t)(sign | 0x7C00u);
+        return (uint16_t)(sign | 0x7E00u | ((a >> 13) & 0x3FFu));
+    }
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);   /* >= 65520 */
+    if (a < 0x38800000u) {                        /* fp16 subnormal range */
+        if (a < 0x33000000u) return (uint16_t)sign;             /* < 2^-25 */
+        uint32_t e = a >> 23;
+        uint32_t m = (a & 0x7FFFFFu) | 0x800000u;
+        uint32_t shift = 126u - e;                /* 14 .. 24 */
+        uint32_t q = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t r = a - 0x38000000u;                 /* rebias 127 -> 15 */
+    r += 0xFFFu + ((r >> 13) & 1u);
+    return (uint16_t)(sign | (r >> 13));
+}
+
+/* ------------------------------------------------------------------------ */
+/* synthetic generator (this build's; the HIP twin lives in synth.hip)      */
+/* ------------------------------------------------------------------------ */
+#define ORC_GAMMA 0x9E3779B97F4A7C15ull
+
+static inline uint64_t fmix64(uint64_t z)
+{
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+uint64_t orc_stream_key(uint64_t seed, uint64_t stream)
+{
+    return fmix64(seed * ORC_GAMMA + fmix64(stream + ORC_GAMMA));
+}
+
+uint64_t orc_rand64(uint64_t key, uint64_t i) { return fmix64(key + (i + 1) * ORC_GAMMA); }
+
+/* natural log on (0,1], argument split m*2^e, atanh series (fmaf chain) */
+static float det_log(float u)
+{
+    uint32_t b = f2u(u);
+    int e = (int)(b >> 23) - 127;
+    float m = u2f((b & 0x7FFFFFu) | 0x3F800000u);
+    if (m > 1.41421356f) { m = m * 0.5f; e += 1; }
+    float f = m - 1.0f;
+    float s = f / (2.0f + f);
+    float z = s * s;
+    float p = 0.13333333f;
+    p = fmaf(p, z, 0.15384615f);
+    p = fmaf(p, z, 0.18181818f);
+    p = fmaf(p, z, 0.22222222f);
+    p = fmaf(p, z, 0.28571429f);
+    p = fmaf(p, z, 0.4f);
+    p = fmaf(p, z, 0.66666667f);
+    float lnm = fmaf(s * z, p, 2.0f * s);
+    float fe = (float)e;
+    return fmaf(fe, 0.693145751953125f, fmaf(fe, 1.42860677e-06f, lnm));
+}
+
+/* cos(2*pi*t) for t in [0,1): quadrant folding + Taylor series to a^14 */
+static float det_cos2pi(float t)
+{
+    float y = t - 0.5f;
+    float sign = -1.0f;
+    y = fabsf(y);
+    if (y > 0.25f) { y = 0.5f - y; sign = -sign; }
+    float a = y * 6.28318531f;
+    float a2 = a * a;
+    float c = -1.1470746e-11f;
+    c = fmaf(c, a2, 2.0876757e-09f);
+    c = fmaf(c, a2, -2.7557319e-07f);
+    c = fmaf(c, a2, 2.4801587e-05f);
+    c = fmaf(c, a2, -1.3888889e-03f);
+    c = fmaf(c, a2, 4.1666668e-02f);
+    c = fmaf(c, a2, -0.5f);
+    c = fmaf(c, a2, 1.0f);
+    return sign * c;
+}
+
+/* Box-Muller (cosine branch) on two 24-bit uniforms of one 64-bit draw */
+float orc_normal(uint64_t key, uint64_t i)
+{
+    uint64_t h = orc_rand64(key, i);
+    float u1 = (float)((h >> 40) + 1u) * 5.9604644775390625e-8f;        /* (0,1] */
+    float u2 = (float)((h >> 16) & 0xFFFFFFu) * 5.9604644775390625e-8f; /* [0,1) */
+    float r = sqrtf(-2.0f * det_log(u1));
+    return r * det_cos2pi(u2);
+}
+
+void orc_gen_normal(float* out, size_t n, uint64_t seed, uint64_t stream, float stddev)
+{
+    uint64_t key = orc_stream_key(seed, stream);
+    for (size_t i = 0; i < n; ++i) out[i] = orc_normal(key, i) * stddev;
+}
+
+void orc_gen_bf16(uint16_t* out, size_t n, uint64_t seed, uint64_t stream, float stddev)
+{
+    uint64_t key = orc_stream_key(seed, stream);
+    for (size_t i = 0; i < n; ++i) out[i] = orc_f32_to_bf16(orc_normal(key, i) * stddev);
+}
+
+/* ------------------------------------------------------------------------ */
+/* A4: SMOE-Q4 (scripts/shatter_moe.py:331-368; kernels.metal:90-105)       */
+/* ------------------------------------------------------------------------ */
+void orc_quantize_q4(const float* w, size_t n, uint32_t group, uint8_t* packed, uint16_t* scales)
+{
+    size_t n_groups = (n + group - 1) / group;             /* :341-345 zero pad */
+    memset(packed, 0, (n + 1) / 2);
+    for (size_t g = 0; g < n_groups; ++g) {
+        size_t base = g * (size_t)group;
+        float absmax = 0.0f;                               /* :350 */
+        for (uint32_t j = 0; j < group; ++j) {
+            float v = (base + j < n) ? w[base + j] : 0.0f;
+            float a = fabsf(v);
+            if (a > absmax) absmax = a;
+        }
+        float best = (absmax == 0.0f) ? 1.0f : absmax;     /* :351 */
+        scales[g] = orc_f32_to_f16(best);                  /* :352 */
+        for (uint32_t j = 0; j < group && base + j < n; ++j) {
+            float q = w[base + j] / best;                  /* :355 */
+            q = q * 7.5f;
+            q = q + 7.5f;                                  /* :356 */
+            float r = rintf(q);                            /* np.round: half-even */
+            int c = (int)r;
+            if (c < 0) c = 0;
+            if (c > 15) c = 15;
+            size_t i = base + j;                           /* :361-365 low nibble even */
+            packed[i >> 1] |= (uint8_t)((uint32_t)c << ((i & 1u) * 4u));
+        }
+    }
+}
+
+float orc_dequant_q4(const uint8_t* packed, const uint16_t* scales, size_t wi, uint32_t group)
+{
+    uint32_t code = ((uint32_t)packed[wi >> 1] >> ((wi & 1u) * 4u)) & 0xFu;
+    float scale = orc_f16_to_f32(scales[wi / group]);
+    return ((float)code - 7.5f) * (1.0f / 7.5f) * scale;  /* kernels.metal:104 */
+}
+
+void orc_dequant_q4_all(const uint8_t* packed, const uint16_t* scales, size_t n,
+                        uint32_t group, float* out)
+{
+    for (size_t i = 0; i < n; ++i) out[i] = orc_dequant_q4(packed, scales, i, group);
+}
+
+void orc_synth_q4(uint8_t* packed, uint16_t* scales, uint32_t rows, uint32_t cols,
+                  uint32_t group, uint64_t seed, uint64_t stream, float stddev)
+{
+    size_t n = (size_t)rows * cols;
+    float* w = (float*)malloc(n * sizeof(float));
+    if (!w) return;
+    orc_gen_normal(w, n, seed, stream, stddev);
+    orc_quantize_q4(w, n, group, packed, scales);
+    free(w);
+}
+
+/* ------------------------------------------------------------------------ */
+/* A1, A2, A8 (src/common.hpp)                                               */
+/* ------------------------------------------------------------------------ */
+void orc_rms_norm_bf16(float* x, const uint16_t* w, uint32_t n)   /* :245-256 */
+{
+    float ss = 0.0f;
+    for (uint32_t i = 0; i < n; ++i) ss += x[i] * x[i];
+    ss /= (float)n;
+    ss += 1e-6f;
+    ss = 1.0f / sqrtf(ss);
+    for (uint32_t i = 0; i < n; ++i) x[i] = (x[i] * ss) * orc_bf16_to_f32(w[i]);
+}
+
+void orc_matvec_bf16(float* out, const uint16_t* weight, const float* in,
+                     uint32_t rows, uint32_t cols)                 /* :293-306 */
+{
+    for (uint32_t i = 0; i < rows; ++i) {
+        float sum = 0.0f;
+        const uint16_t* w_row = weight + (size_t)i * cols;
+        for (uint32_t j = 0; j < cols; ++j) sum += orc_bf16_to_f32(w_row[j]) * in[j];
+        out[i] = sum;
+    }
+}
+
+void orc_axpy_f32(float* y, float a, const float* x, uint32_t n)   /* :346-349 */
+{
+    for (uint32_t i = 0; i < n; ++i) y[i] += a * x[i];
+}
+
+/* ------------------------------------------------------------------------ */
+/* A3: softmax + partial selection sort with swaps (scout.cpp:77-123)       */
+/* ------------------------------------------------------------------------ */
+uint32_t orc_top_k(const float* scores, uint32_t n, uint32_t k,
+                   uint32_t* out_indices, float* out_weights, int norm_topk)
+{
+    uint32_t count = k < n ? k : n;
+    float* tmp = (float*)malloc((n ? n : 1) * sizeof(float));
+    uint32_t* idx = (uint32_t*)malloc((n ? n : 1) * sizeof(uint32_t));
+    if (!tmp || !idx) { free(tmp); free(idx); return 0; }
+
+    float max_val = scores[0];
+    for (uint32_t i = 1; i < n; ++i)
+        if (scores[i] > max_val) max_val = scores[i];
+    float sum_exp = 0.0f;
+    for (uint32_t i = 0; i < n; ++i) {
+        tmp[i] = expf(scores[i] - max_val);
+        idx[i] = i;
+        sum_exp += tmp[i];
+    }
+    float inv_sum = (sum_exp > 0.0f) ? 1.0f / sum_exp : 0.0f;
+    for (uint32_t i = 0; i < n; ++i) tmp[i] *= inv_sum;
+
+    for (uint32_t s = 0; s < count; ++s) {
+        uint32_t best = s;
+        for (uint32_t i = s + 1; i < n; ++i)
+            if (tmp[i] > tmp[best]) best = i;
+        float ft = tmp[s]; tmp[s] = tmp[best]; tmp[best] = ft;
+        uint32_t it = idx[s]; idx[s] = idx[best]; idx[best] = it;
+        out_indices[s] = idx[s];
+        if (out_weights) out_weights[s] = tmp[s];
+    }
+
+    if (norm_topk && out_weights) {
+        float topk_sum = 0.0f;
+        for (uint32_t s = 0; s < count; ++s) topk_sum += out_weights[s];
+        if (topk_sum > 0.0f) {
+            float inv = 1.0f / topk_sum;
+            for (uint32_t s = 0; s < count; ++s) out_weights[s] *= inv;
+        }
+    }
+    free(tmp);
+    free(idx);
+    return count;
+}
+
+/* ------------------------------------------------------------------------ */
+/* A5/A6: expert FFN with per-weight dequant (kernels.metal:61-63, 672-769) */
+/* ------------------------------------------------------------------------ */
+float orc_silu(float x) { return x * (1.0f / (1.0f + expf(-x))); }
+
+/* one row of a Q4 matrix dotted with v, sequential fp32 sum over columns;
+ * the level table holds exactly ((float)c - 7.5f) * (1.0f/7.5f) per code, so
+ * level[c] * scale is the per-weight dequant of kernels.metal:104 */
+static float q4_row_dot(const uint8_t* packed, const uint16_t* scales, size_t row,
+                        uint32_t cols, uint32_t group, const float* v)
+{
+    float level[16];
+    for (int c = 0; c < 16; ++c) level[c] = ((float)c - 7.5f) * (1.0f / 7.5f);
+    float acc = 0.0f;
+    size_t base = row * (size_t)cols;
+    for (uint32_t j0 = 0; j0 < cols; j0 += group) {
+        float s = orc_f16_to_f32(scales[(base + j0) / group]);
+        uint32_t jend = j0 + group < cols ? j0 + group : cols;
+        for (uint32_t j = j0; j < jend; ++j) {
+            size_t wi = base + j;
+            uint32_t code = ((uint32_t)packed[wi >> 1] >> ((wi & 1u) * 4u)) & 0xFu;
+            float w = level[code] * s;
+            acc += w * v[j];
+        }
+    }
+    return acc;
+}
+
+void orc_expert_ffn(const uint8_t* pg, const uint16_t* sg,
+                    const uint8_t* pu, const uint16_t* su,
+                    const uint8_t* pd, const uint16_t* sd,
+                    const float* x, float* hidden, float* out,
+                    uint32_t d_ff, uint32_t d_model, uint32_t group)
+{
+    for (uint32_t r = 0; r < d_ff; ++r) {
+        float g = q4_row_dot(pg, sg, r, d_model, group, x);
+        float u = q4_row_dot(pu, su, r, d_model, group, x);
+        hidden[r] = orc_silu(g) * u;                       /* kernels.metal:720-722 */
+    }
+    for (uint32_t d = 0; d < d_model; ++d)
+        out[d] = q4_row_dot(pd, sd, d, d_ff, group, hidden);
+}
+
+/* ------------------------------------------------------------------------ */
+/* A11: blob layout (shatter_moe.py:627-674): [gate p][gate s][up p][up s]  */
+/* [down p][down s], gate/up [d_ff x d_model], down [d_model x d_ff]         */
+/* ------------------------------------------------------------------------ */
+void orc_blob_layout(uint32_t d_model, uint32_t d_ff, uint32_t group,
+                     uint64_t* off, uint64_t* blob_bytes)
+{
+    uint64_t n = (uint64_t)d_model * d_ff;
+    uint64_t pb = (n + 1) / 2, sb = ((n + group - 1) / group) * 2;
+    off[0] = 0;               off[1] = pb;
+    off[2] = pb + sb;         off[3] = 2 * pb + sb;
+    off[4] = 2 * (pb + sb);   off[5] = 3 * pb + 2 * sb;
+    *blob_bytes = 3 * (pb + sb);
+}
+
+static void expert_ptrs(const OrcLayer* L, uint32_t e, const uint8_t** pg, const uint16_t** sg,
+                        const uint8_t** pu, const uint16_t** su,
+                        const uint8_t** pd, const uint16_t** sd)
+{
+    const uint8_t* b = L->experts + (size_t)e * L->stride;
+    *pg = b + L->gate_packed;  *sg = (const uint16_t*)(b + L->gate_scales);
+    *pu = b + L->up_packed;    *su = (const uint16_t*)(b + L->up_scales);
+    *pd = b + L->down_packed;  *sd = (const uint16_t*)(b + L->down_scales);
+}
+
+/* ------------------------------------------------------------------------ */
+/* A12: decode MoE block (src/decode.cpp:236-238, 280-302, 338-509)         */
+/* ------------------------------------------------------------------------ */
+void orc_moe_decode_layer(const OrcShape* s, const OrcLayer* L, float* hidden,
+                          uint32_t* ids, float* weights, float* logits_out,
+                          float* normed_out, float* expert_out)
+{
+    const uint32_t D = s->d_model, E = s->n_experts, K = s->top_k, I = s->d_ff;
+    float* normed = (float*)malloc(D * sizeof(float));
+    float* logits = (float*)malloc(E * sizeof(float));
+    float* routed = (float*)calloc(D, sizeof(float));
+    float* h = (float*)malloc(I * sizeof(float));
+    float* y = (float*)malloc(D * sizeof(float));
+    float w[32];
+    uint32_t rid[32];
+
+    memcpy(normed, hidden, D * sizeof(float));                 /* :237 */
+    orc_rms_norm_bf16(normed, L->norm_w, D);                   /* :238 */
+    orc_matvec_bf16(logits, L->router_w, normed, E, D);        /* :280-283 */
+    uint32_t nsel = orc_top_k(logits, E, K, rid, w, 0);        /* :290-292 */
+    uint32_t nk = nsel < K ? nsel : K;
+    float w_sum = 0.0f;
+    for (uint32_t e = 0; e < nk; ++e) w_sum += w[e];           /* :296-297 */
+    float w_inv = (s->norm_topk && w_sum > 0.0f) ? 1.0f / w_sum : 1.0f;
+    for (uint32_t e = 0; e < nk; ++e) w[e] = w[e] * w_inv;     /* :301 */
+
+    for (uint32_t e = 0; e < nk; ++e) {                        /* :482-498 */
+        const uint8_t *pg, *pu, *pd; const uint16_t *sg, *su, *sd;
+        expert_ptrs(L, rid[e], &pg, &sg, &pu, &su, &pd, &sd);
+        orc_expert_ffn(pg, sg, pu, su, pd, sd, normed, h, y, I, D, s->group_size);
+        if (expert_out) memcpy(expert_out + (size_t)e * D, y, D * sizeof(float));
+        orc_axpy_f32(routed, w[e], y, D);
+    }
+    for (uint32_t d = 0; d < D; ++d)                           /* :506-509 */
+        hidden[d] += 0.0f + routed[d];
+
+    for (uint32_t e = 0; e < nk; ++e) { ids[e] = rid[e]; weights[e] = w[e]; }
+    if (logits_out) memcpy(logits_out, logits, E * sizeof(float));
+    if (normed_out) memcpy(normed_out, normed, D * sizeof(float));
+    free(normed); free(logits); free(routed); free(h); free(y);
+}
+
+/* ------------------------------------------------------------------------ */
+/* A9: permute (src/prefill.cpp:38-68, 315-332)                              */
+/* ------------------------------------------------------------------------ */
+#define ORC_CHUNK 64u
+#define ORC_MAX_EXPERTS 512u
+typedef struct { uint8_t tok[ORC_CHUNK]; float w[ORC_CHUNK]; uint32_t count; } OrcExpertTokens;
+static OrcExpertTokens g_elist[ORC_MAX_EXPERTS];
+static uint32_t g_union_ids[ORC_MAX_EXPERTS];
+static uint32_t g_union_size;
+
+void orc_union_reset(void) { g_union_size = 0; }
+
+int orc_union_add(uint32_t expert, uint32_t tok_row, float weight)
+{
+    OrcExpertTokens* et = &g_elist[expert];
+    int fresh = 1;
+    for (uint32_t u = 0; u < g_union_size; ++u)
+        if (g_union_ids[u] == expert) { fresh = 0; break; }
+    if (fresh) {
+        et->count = 0;
+        if (g_union_size < ORC_MAX_EXPERTS) g_union_ids[g_union_size++] = expert;
+    }
+    if (et->count < ORC_CHUNK) {
+        et->tok[et->count] = (uint8_t)tok_row;
+        et->w[et->count] = weight;
+        et->count++;
+    }
+    return fresh;
+}
+
+uint32_t orc_union_size(void) { return g_union_size; }
+uint32_t orc_union_id(uint32_t u) { return g_union_ids[u]; }
+uint32_t orc_union_count(uint32_t e) { return g_elist[e].count; }
+uint32_t orc_union_tok(uint32_t e, uint32_t t) { return g_elist[e].tok[t]; }
+float    orc_union_w(uint32_t e, uint32_t t) { return g_elist[e].w[t]; }
+
+uint32_t orc_permute(const uint32_t* ids, const float* w, uint32_t T, uint32_t k,
+                     uint32_t n_experts, uint32_t* offsets, uint32_t* tok,
+                     float* wout, uint32_t* union_ids)
+{
+    uint32_t* cnt = (uint32_t*)calloc(n_experts + 1, sizeof(uint32_t));
+    uint8_t* seen = (uint8_t*)calloc(n_experts, 1);
+    uint32_t nu = 0;
+    for (uint32_t p = 0; p < T * k; ++p) {
+        uint32_t e = ids[p];
+        cnt[e + 1]++;
+        if (!seen[e]) { seen[e] = 1; union_ids[nu++] = e; }
+    }
+    for (uint32_t e = 0; e < n_experts; ++e) cnt[e + 1] += cnt[e];
+    memcpy(offsets, cnt, (n_experts + 1) * sizeof(uint32_t));
+    for (uint32_t p = 0; p < T * k; ++p) {               /* token-major: stable */
+        uint32_t e = ids[p];
+        uint32_t dst = cnt[e]++;
+        tok[dst] = p / k;
+        wout[dst] = w[p];
+    }
+    free(cnt); free(seen);
+    return nu;
+}
+
+/* ------------------------------------------------------------------------ */
+/* A10: prefill MoE block (src/prefill.cpp:269-276, 308-453), chunks of 64  */
+/* ------------------------------------------------------------------------ */
+void orc_moe_prefill_layer(const OrcShape* s, const OrcLayer* L, float* hidden,
+                           uint32_t T, uint32_t* ids_out, float* w_out)
+{
+    const uint32_t D = s->d_model, E = s->n_experts, K = s->top_k, I = s->d_ff;
+    float* normed = (float*)malloc((size_t)ORC_CHUNK * D * sizeof(float));
+    float* routed = (float*)malloc((size_t)ORC_CHUNK * D * sizeof(float));
+    float* logits = (float*)malloc(E * sizeof(float));
+    float* h = (float*)malloc(I * sizeof(float));
+    float* y = (float*)malloc(D * sizeof(float));
+    uint32_t tid[32];
+    float tw[32];
+
+    for (uint32_t c0 = 0; c0 < T; c0 += ORC_CHUNK) {
+        uint32_t B = (T - c0 < ORC_CHUNK) ? T - c0 : ORC_CHUNK;
+        for (uint32_t i = 0; i < B; ++i) {                       /* :272-275 */
+            memcpy(normed + (size_t)i * D, hidden + (size_t)(c0 + i) * D, D * sizeof(float));
+            orc_rms_norm_bf16(normed + (size_t)i * D, L->norm_w, D);
+        }
+        orc_union_reset();                                       /* :314 */
+        memset(routed, 0, (size_t)B * D * sizeof(float));        /* :315 */
+        for (uint32_t i = 0; i < B; ++i) {                       /* :319-332 */
+            orc_matvec_bf16(logits, L->router_w, normed + (size_t)i * D, E, D);
+            uint32_t cnt = orc_top_k(logits, E, K, tid, tw, (int)s->norm_topk);
+            for (uint32_t e = 0; e < cnt; ++e) {
+                ids_out[(size_t)(c0 + i) * K + e] = tid[e];
+                w_out[(size_t)(c0 + i) * K + e] = tw[e];
+                if (tid[e] < ORC_MAX_EXPERTS) orc_union_add(tid[e], i, tw[e]);
+            }
+        }
+        for (uint32_t u = 0; u < g_union_size; ++u) {            /* :339-417 */
+            uint32_t eid = g_union_ids[u];
+            const OrcExpertTokens* et = &g_elist[eid];
+            const uint8_t *pg, *pu, *pd; const uint16_t *sg, *su, *sd;
+            expert_ptrs(L, eid, &pg, &sg, &pu, &su, &pd, &sd);
+            for (uint32_t t = 0; t < et->count; ++t) {
+                orc_expert_ffn(pg, sg, pu, su, pd, sd, normed + (size_t)et->tok[t] * D,
+                               h, y, I, D, s->group_size);
+                float* ro = routed + (size_t)et->tok[t] * D;     /* :380-385 */
+                const float wt = et->w[t];
+                for (uint32_t d = 0; d < D; ++d) ro[d] += wt * y[d];
+            }
+        }
+        for (uint32_t i = 0; i < B; ++i) {                       /* :446-451 */
+            float* hh = hidden + (size_t)(c0 + i) * D;
+            const float* ro = routed + (size_t)i * D;
+            for (uint32_t d = 0; d < D; ++d) hh[d] += ro[d];
+        }
+    }
+    free(normed); free(routed); free(logits); free(h); free(y);
+}

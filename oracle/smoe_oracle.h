@@ -1,0 +1,139 @@
+/*
+ * smoe_oracle.h -- CPU restatement of S-MoE's per-layer MoE arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (the HIP library, the
+ * host C++ layer, the Python binding) links, loads or calls this code.  It is
+ * used by tests/, by __graft_entry__.smoke() as the checker and by bench.py's
+ * cpu_baseline leg (timed, reported beside the GPU number).
+ *
+ * Every function restates one piece of the reference (paths relative to the
+ * reference tree) and is pinned as noted:
+ *   orc_bf16_to_f32 / orc_rms_norm_bf16 / orc_matvec_bf16 / orc_axpy_f32
+ *       src/common.hpp:238-256, 293-306, 346-349
+ *       pinned: golden vectors from the compiled reference (oracle/_ref).
+ *   orc_top_k   src/scout/scout.cpp:77-123
+ *       pinned: golden vectors from the compiled reference incl. constructed
+ *       ties; brute-force swap-sort equivalence.
+ *   orc_quantize_q4 / orc_dequant_q4   scripts/shatter_moe.py:331-387,
+ *       src/compute/kernels.metal:90-105
+ *       pinned: known-answer tests (+-absmax -> 15/0, half-even ties, zero
+ *       group, nibble order, reconstruction bound), numpy float16 cast.
+ *   orc_expert_ffn   kernels.metal:61-63, 308-365, 672-769
+ *       pinned: fp64 brute force on tiny shapes, dequant identity, zero
+ *       input, scale linearity.  (The reference's FFN exists only as Metal
+ *       shaders; no reference-held vectors exist.)
+ *   orc_moe_decode_layer   src/decode.cpp:236-238, 280-302, 338-509
+ *   orc_permute / orc_union_*   src/prefill.cpp:38-68, 315-332
+ *       pinned: compiled reference union_add vectors; brute-force stable sort.
+ *   orc_moe_prefill_layer  src/prefill.cpp:308-453
+ *   orc_rand_* / orc_normal   synthetic-input generator of this build (not in
+ *       the reference); the HIP generator must reproduce it bit for bit.
+ */
+#ifndef SMOE_ORACLE_H
+#define SMOE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- number formats ------------------------------------------------------ */
+float    orc_bf16_to_f32(uint16_t b);
+uint16_t orc_f32_to_bf16(float f);          /* round to nearest even */
+float    orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);           /* round to nearest even */
+
+/* ---- synthetic generator (counter based, bit-reproducible on the GPU) ---- */
+uint64_t orc_stream_key(uint64_t seed, uint64_t stream);
+uint64_t orc_rand64(uint64_t key, uint64_t i);
+float    orc_normal(uint64_t key, uint64_t i);
+void     orc_gen_normal(float* out, size_t n, uint64_t seed, uint64_t stream,
+                        float stddev);
+void     orc_gen_bf16(uint16_t* out, size_t n, uint64_t seed, uint64_t stream,
+                      float stddev);
+
+/* ---- A4: SMOE-Q4 ---------------------------------------------------------- */
+/* packed: n/2 bytes (low nibble = even index); scales: n/group fp16 bits */
+void  orc_quantize_q4(const float* w, size_t n, uint32_t group,
+                      uint8_t* packed, uint16_t* scales);
+float orc_dequant_q4(const uint8_t* packed, const uint16_t* scales,
+                     size_t wi, uint32_t group);
+void  orc_dequant_q4_all(const uint8_t* packed, const uint16_t* scales,
+                         size_t n, uint32_t group, float* out);
+/* synthetic expert matrix: N(0,stddev) from (seed, stream) then quantize */
+void  orc_synth_q4(uint8_t* packed, uint16_t* scales, uint32_t rows,
+                   uint32_t cols, uint32_t group, uint64_t seed,
+                   uint64_t stream, float stddev);
+
+/* ---- A1, A2, A8 ------------------------------------------------------------ */
+void orc_rms_norm_bf16(float* x, const uint16_t* w, uint32_t n);
+void orc_matvec_bf16(float* out, const uint16_t* weight, const float* in,
+                     uint32_t rows, uint32_t cols);
+void orc_axpy_f32(float* y, float a, const float* x, uint32_t n);
+
+/* ---- A3 ------------------------------------------------------------------ */
+uint32_t orc_top_k(const float* scores, uint32_t n, uint32_t k,
+                   uint32_t* out_indices, float* out_weights, int norm_topk);
+
+/* ---- A5/A6: one expert, per-weight dequant, sequential fp32 sums ---------- */
+float orc_silu(float x);
+void orc_expert_ffn(const uint8_t* pg, const uint16_t* sg,
+                    const uint8_t* pu, const uint16_t* su,
+                    const uint8_t* pd, const uint16_t* sd,
+                    const float* x, float* hidden, float* out,
+                    uint32_t d_ff, uint32_t d_model, uint32_t group);
+
+/* ---- A11: resident expert pool addressing -------------------------------- */
+typedef struct {
+    uint32_t d_model, n_experts, top_k, d_ff, group_size, norm_topk;
+} OrcShape;
+
+typedef struct {
+    const uint16_t* norm_w;      /* [d_model] bf16 */
+    const uint16_t* router_w;    /* [n_experts x d_model] bf16 */
+    const uint8_t*  experts;     /* blob of expert 0 */
+    uint64_t        stride;      /* bytes between consecutive expert blobs */
+    uint64_t gate_packed, gate_scales, up_packed, up_scales,
+             down_packed, down_scales;   /* offsets inside a blob */
+} OrcLayer;
+
+/* blob layout of shatter_moe.py build_expert_blob (:627-674) for one shape */
+void orc_blob_layout(uint32_t d_model, uint32_t d_ff, uint32_t group,
+                     uint64_t* offsets6, uint64_t* blob_bytes);
+
+/* ---- A12: one decode MoE block (RMSNorm -> router -> top-k -> FFN ->
+ *      rank-ordered combine -> residual).  hidden is updated in place.
+ *      ids/weights [top_k]; optional logits [n_experts], normed [d_model],
+ *      expert_out [top_k x d_model]; any optional pointer may be NULL. ---- */
+void orc_moe_decode_layer(const OrcShape* s, const OrcLayer* L, float* hidden,
+                          uint32_t* ids, float* weights, float* logits,
+                          float* normed, float* expert_out);
+
+/* ---- A9: token-by-expert permute ----------------------------------------- */
+/* Whole-prompt stable counting sort of (token, rank) pairs by expert id:
+ *   offsets[n_experts+1], tok[T*k], w[T*k] (ascending token order inside
+ *   each expert), union_ids[<=n_experts] in order of first appearance
+ *   (token-major, rank-minor); returns the union size.                     */
+uint32_t orc_permute(const uint32_t* ids, const float* w, uint32_t T,
+                     uint32_t k, uint32_t n_experts, uint32_t* offsets,
+                     uint32_t* tok, float* wout, uint32_t* union_ids);
+/* prefill.cpp union_add restated: per-chunk state machine */
+void     orc_union_reset(void);
+int      orc_union_add(uint32_t expert, uint32_t tok_row, float weight);
+uint32_t orc_union_size(void);
+uint32_t orc_union_id(uint32_t u);
+uint32_t orc_union_count(uint32_t expert);
+uint32_t orc_union_tok(uint32_t expert, uint32_t t);
+float    orc_union_w(uint32_t expert, uint32_t t);
+
+/* ---- A10: prefill MoE block over T tokens, layer-major in chunks of 64 ---
+ *      hidden [T x d_model] updated in place; ids/weights [T x top_k]. ---- */
+void orc_moe_prefill_layer(const OrcShape* s, const OrcLayer* L, float* hidden,
+                           uint32_t T, uint32_t* ids, float* weights);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,647 @@
+// bridge.cpp -- C ABI of the MI355X MoE backend (include/smoe_hip.h).
+//
+// Implements the reference's compute-backend surface (metal_bridge.h, whose
+// Metal implementation is src/compute/metal_bridge.mm) on HIP, plus the
+// device-resident entry points.  The context owns one HIP stream (or uses the
+// caller's), pre-allocated scratch, and a ring of events backing the
+// monotonically increasing handles of the reference (metal_bridge.mm:423-429).
+#include "../../include/smoe_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "kernels.hpp"
+
+using smoe::ExpertPtrs;
+using smoe::LayerDesc;
+using smoe::MoeDims;
+
+namespace {
+
+constexpr uint32_t kSlots = SMOE_MAX_ACTIVE;   // scratch regions (metal_bridge.mm:205-210)
+constexpr uint32_t kEvents = 256;              // handle ring
+
+struct DeviceScratch {
+    // capacities
+    uint32_t D = 0, E = 0, K = 0, I = 0, T = 0;
+    float* normed = nullptr;     // [T x D]
+    float* logits = nullptr;     // [T x E]
+    uint32_t* ids = nullptr;     // [T x K]
+    float* w = nullptr;          // [T x K]
+    ExpertPtrs* tbl = nullptr;   // [T x K]
+    uint32_t* counters = nullptr;// [T]
+    float* h = nullptr;          // [T x K x I]
+};
+
+}  // namespace
+
+struct SmoeMetalCtx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    size_t slot_bytes = 0;
+    uint32_t max_rows = 0;
+
+    // reference-surface scratch (metal_bridge.mm:205-217, :269-272)
+    float* d_input = nullptr;        // [SMOE_MAX_DIM]
+    float* d_hidden = nullptr;       // [kSlots x max_rows]
+    float* d_output = nullptr;       // [kSlots x max_rows]
+    float* d_batch_in = nullptr;     // [64 x 16384]
+    float* d_batch_hidden = nullptr;
+    float* d_batch_out = nullptr;
+    ExpertPtrs* d_tbl_ref = nullptr; // [kSlots]
+
+    hipEvent_t ev[kEvents] = {};
+    uint64_t seq = 0;
+    std::atomic<uint64_t> dispatches{0};
+
+    DeviceScratch ds;
+    std::vector<std::pair<uintptr_t, size_t>> registered;
+    char last_err[256] = {0};
+
+    // per-kernel event timing
+    struct ProfSlot {
+        hipEvent_t a = nullptr, b = nullptr;
+        uint32_t kind = 0;
+        bool pending = false;
+    };
+    bool profiling = false;
+    std::vector<ProfSlot> prof;
+    size_t prof_head = 0;
+    uint64_t prof_launches[SMOE_KERNEL_KINDS] = {};
+    double prof_ms[SMOE_KERNEL_KINDS] = {};
+    int prof_open = -1;   // slot index between prof_begin and prof_end
+};
+
+namespace {
+
+bool hip_ok(SmoeMetalCtx* ctx, hipError_t e, const char* what)
+{
+    if (e == hipSuccess) return true;
+    if (ctx) std::snprintf(ctx->last_err, sizeof(ctx->last_err), "%s: %s", what, hipGetErrorString(e));
+    std::fprintf(stderr, "[smoe_hip] %s failed: %s\n", what, hipGetErrorString(e));
+    return false;
+}
+
+template <typename T>
+bool dalloc(SmoeMetalCtx* ctx, T** p, size_t count)
+{
+    *p = nullptr;
+    if (count == 0) count = 1;
+    return hip_ok(ctx, hipMalloc(reinterpret_cast<void**>(p), count * sizeof(T)), "hipMalloc");
+}
+
+template <typename T>
+void dfree(T*& p)
+{
+    if (p) (void)hipFree(p);
+    p = nullptr;
+}
+
+void free_device_scratch(DeviceScratch& s)
+{
+    dfree(s.normed);
+    dfree(s.logits);
+    dfree(s.ids);
+    dfree(s.w);
+    dfree(s.tbl);
+    dfree(s.counters);
+    dfree(s.h);
+    s = DeviceScratch{};
+}
+
+// reference-surface shape check (kernels.metal:146-152, metal_bridge.mm:460-461)
+bool ref_shape_ok(const SmoeMetalCtx* ctx, uint32_t gate_rows, uint32_t gate_cols, uint32_t down_rows,
+                  uint32_t down_cols, uint32_t group_size, uint32_t bits)
+{
+    if (bits != 4) return false;
+    if (group_size == 0 || group_size % 32 != 0 || group_size > 128 || (group_size & (group_size - 1))) return false;
+    if (gate_rows != down_cols || gate_cols != down_rows) return false;
+    if (gate_cols == 0 || gate_rows == 0) return false;
+    if (gate_cols % group_size || gate_rows % group_size) return false;
+    if (gate_cols > SMOE_MAX_DIM || gate_rows > SMOE_MAX_DIM) return false;
+    if (ctx && (gate_rows > ctx->max_rows || down_rows > ctx->max_rows)) return false;
+    return true;
+}
+
+int shape_check(const SmoeMoeShape* s)
+{
+    if (!s) return SMOE_ERR_ARG;
+    if (s->bits != 4) return SMOE_ERR_BITS;
+    const uint32_t g = s->group_size;
+    if (g == 0 || g % 32 != 0 || g > 128 || (g & (g - 1))) return SMOE_ERR_SHAPE;
+    if (s->d_model == 0 || s->d_ff == 0 || s->n_experts == 0 || s->top_k == 0) return SMOE_ERR_SHAPE;
+    if (s->d_model % 64 || s->d_ff % 64 || s->d_model % g || s->d_ff % g) return SMOE_ERR_SHAPE;
+    if (s->d_model > SMOE_MAX_DIM || s->d_ff > SMOE_MAX_DIM) return SMOE_ERR_SHAPE;
+    if (s->top_k > SMOE_MAX_ACTIVE || s->top_k > s->n_experts) return SMOE_ERR_SHAPE;
+    if (s->n_experts > SMOE_MAX_EXPERTS) return SMOE_ERR_SHAPE;
+    if (static_cast<uint64_t>(s->top_k) * (s->d_ff / 32) > 8ull * 64 * 4) return SMOE_ERR_SHAPE;
+    return SMOE_OK;
+}
+
+MoeDims dims_of(const SmoeMoeShape* s)
+{
+    return MoeDims{s->d_model, s->n_experts, s->top_k, s->d_ff, s->group_size, s->norm_topk ? 1u : 0u};
+}
+
+LayerDesc layer_of(const SmoeMoeLayer* L)
+{
+    LayerDesc d;
+    d.norm_w = L->norm_w;
+    d.router_w = L->router_w;
+    d.experts = L->experts;
+    d.stride = L->expert_stride;
+    d.off[0] = L->gate_packed_offset;
+    d.off[1] = L->gate_scales_offset;
+    d.off[2] = L->up_packed_offset;
+    d.off[3] = L->up_scales_offset;
+    d.off[4] = L->down_packed_offset;
+    d.off[5] = L->down_scales_offset;
+    return d;
+}
+
+bool stream_capturing(hipStream_t s)
+{
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) return false;
+    return st != hipStreamCaptureStatusNone;
+}
+
+int ensure_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
+{
+    DeviceScratch& c = ctx->ds;
+    if (c.normed && c.D >= s->d_model && c.E >= s->n_experts && c.K >= s->top_k && c.I >= s->d_ff && c.T >= T)
+        return SMOE_OK;
+    if (stream_capturing(ctx->stream)) return SMOE_ERR_CAPTURE;
+    if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
+    DeviceScratch n;
+    n.D = std::max(c.D, s->d_model);
+    n.E = std::max(c.E, s->n_experts);
+    n.K = std::max(c.K, s->top_k);
+    n.I = std::max(c.I, s->d_ff);
+    n.T = std::max(c.T, T);
+    free_device_scratch(c);
+    const size_t T_ = n.T;
+    bool ok = dalloc(ctx, &n.normed, T_ * n.D) && dalloc(ctx, &n.logits, T_ * n.E) &&
+              dalloc(ctx, &n.ids, T_ * n.K) && dalloc(ctx, &n.w, T_ * n.K) && dalloc(ctx, &n.tbl, T_ * n.K) &&
+              dalloc(ctx, &n.counters, T_) && dalloc(ctx, &n.h, T_ * n.K * n.I);
+    if (!ok) {
+        free_device_scratch(n);
+        return SMOE_ERR_HIP;
+    }
+    // counters start at zero; every k_route launch leaves them at zero again
+    if (!hip_ok(ctx, hipMemset(n.counters, 0, T_ * sizeof(uint32_t)), "hipMemset")) {
+        free_device_scratch(n);
+        return SMOE_ERR_HIP;
+    }
+    c = n;
+    return SMOE_OK;
+}
+
+constexpr size_t kProfSlots = 4096;
+
+void prof_flush_slot(SmoeMetalCtx* ctx, SmoeMetalCtx::ProfSlot& p)
+{
+    if (!p.pending) return;
+    float ms = 0.f;
+    if (hipEventSynchronize(p.b) == hipSuccess && hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+        ctx->prof_launches[p.kind] += 1;
+        ctx->prof_ms[p.kind] += ms;
+    }
+    p.pending = false;
+}
+
+// bracket one kernel launch with timing events (no-op unless profiling and
+// the stream is not being captured)
+void prof_begin(SmoeMetalCtx* ctx, uint32_t kind)
+{
+    ctx->prof_open = -1;
+    if (!ctx->profiling || stream_capturing(ctx->stream)) return;
+    const size_t i = ctx->prof_head % kProfSlots;
+    auto& p = ctx->prof[i];
+    prof_flush_slot(ctx, p);
+    p.kind = kind;
+    if (hipEventRecord(p.a, ctx->stream) == hipSuccess) ctx->prof_open = static_cast<int>(i);
+}
+
+void prof_end(SmoeMetalCtx* ctx)
+{
+    if (ctx->prof_open < 0) return;
+    auto& p = ctx->prof[ctx->prof_open];
+    if (hipEventRecord(p.b, ctx->stream) == hipSuccess) {
+        p.pending = true;
+        ctx->prof_head++;
+    }
+    ctx->prof_open = -1;
+}
+
+// launch helper: times the launch when profiling
+template <typename F>
+bool timed(SmoeMetalCtx* ctx, uint32_t kind, const char* what, F&& launch)
+{
+    prof_begin(ctx, kind);
+    const hipError_t e = launch();
+    prof_end(ctx);
+    return hip_ok(ctx, e, what);
+}
+
+void* record_handle(SmoeMetalCtx* ctx)
+{
+    const uint64_t h = ++ctx->seq;
+    if (!hip_ok(ctx, hipEventRecord(ctx->ev[h % kEvents], ctx->stream), "hipEventRecord")) return nullptr;
+    return reinterpret_cast<void*>(static_cast<uintptr_t>(h));
+}
+
+bool wait_handle(SmoeMetalCtx* ctx, void* handle)
+{
+    const uint64_t h = static_cast<uint64_t>(reinterpret_cast<uintptr_t>(handle));
+    if (h == 0 || h > ctx->seq) return false;
+    // An event older than the ring was re-recorded by later work on the same
+    // in-order stream; waiting for that later work also covers `h`.
+    return hip_ok(ctx, hipEventSynchronize(ctx->ev[h % kEvents]), "hipEventSynchronize");
+}
+
+// one group of same-shaped experts on ctx->d_input (reference surface)
+void* dispatch_group(SmoeMetalCtx* ctx, const ExpertPtrs* tbl_host, uint32_t n, const float* input_vec,
+                     uint32_t gate_rows, uint32_t gate_cols, uint32_t group_size)
+{
+    const MoeDims d{gate_cols, 0, n, gate_rows, group_size, 0};
+    if (!hip_ok(ctx, hipMemcpyAsync(ctx->d_input, input_vec, gate_cols * sizeof(float), hipMemcpyHostToDevice,
+                                    ctx->stream), "hipMemcpyAsync(input)"))
+        return nullptr;
+    if (!hip_ok(ctx, hipMemcpyAsync(ctx->d_tbl_ref, tbl_host, n * sizeof(ExpertPtrs), hipMemcpyHostToDevice,
+                                    ctx->stream), "hipMemcpyAsync(table)"))
+        return nullptr;
+    if (!timed(ctx, SMOE_KERNEL_GATE_UP, "gate_up", [&] {
+            return smoe::launch_gate_up(d, ctx->d_tbl_ref, n, ctx->d_input, ctx->d_hidden, ctx->max_rows, 1, 0, 0, 0,
+                                        ctx->stream);
+        }))
+        return nullptr;
+    if (!timed(ctx, SMOE_KERNEL_DOWN_SLOTS, "down", [&] {
+            return smoe::launch_down_slots(d, ctx->d_tbl_ref, n, ctx->d_hidden, ctx->max_rows, ctx->d_output,
+                                           ctx->max_rows, 1, 0, 0, 0, ctx->stream);
+        }))
+        return nullptr;
+    ctx->dispatches.fetch_add(n, std::memory_order_relaxed);
+    return record_handle(ctx);
+}
+
+}  // namespace
+
+// ============================================================================
+// 1. reference surface
+// ============================================================================
+extern "C" SmoeMetalCtx* smoe_metal_init(size_t slot_bytes)
+{
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
+        std::fprintf(stderr, "[smoe_hip] ERROR: no HIP device.\n");
+        return nullptr;
+    }
+    SmoeMetalCtx* ctx = new SmoeMetalCtx();
+    if (hipGetDevice(&ctx->device) != hipSuccess) ctx->device = 0;
+    ctx->slot_bytes = slot_bytes;
+    ctx->max_rows = static_cast<uint32_t>(std::min(slot_bytes / sizeof(float), size_t(32768)));
+    if (ctx->max_rows < SMOE_MAX_DIM) ctx->max_rows = SMOE_MAX_DIM;
+    const size_t plane = size_t(SMOE_MAX_FFN_BATCH) * SMOE_MAX_FFN_BATCH_DIM;
+    bool ok = hip_ok(ctx, hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking), "hipStreamCreate") &&
+              dalloc(ctx, &ctx->d_input, SMOE_MAX_DIM) && dalloc(ctx, &ctx->d_hidden, size_t(kSlots) * ctx->max_rows) &&
+              dalloc(ctx, &ctx->d_output, size_t(kSlots) * ctx->max_rows) && dalloc(ctx, &ctx->d_batch_in, plane) &&
+              dalloc(ctx, &ctx->d_batch_hidden, plane) && dalloc(ctx, &ctx->d_batch_out, plane) &&
+              dalloc(ctx, &ctx->d_tbl_ref, kSlots);
+    for (uint32_t i = 0; ok && i < kEvents; ++i)
+        ok = hip_ok(ctx, hipEventCreateWithFlags(&ctx->ev[i], hipEventDisableTiming), "hipEventCreate");
+    if (!ok) {
+        smoe_metal_destroy(ctx);
+        return nullptr;
+    }
+    ctx->stream = ctx->own_stream;
+    return ctx;
+}
+
+extern "C" void smoe_metal_destroy(SmoeMetalCtx* ctx)
+{
+    if (!ctx) return;
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->own_stream && ctx->own_stream != ctx->stream) (void)hipStreamSynchronize(ctx->own_stream);
+    free_device_scratch(ctx->ds);
+    dfree(ctx->d_input);
+    dfree(ctx->d_hidden);
+    dfree(ctx->d_output);
+    dfree(ctx->d_batch_in);
+    dfree(ctx->d_batch_hidden);
+    dfree(ctx->d_batch_out);
+    dfree(ctx->d_tbl_ref);
+    for (uint32_t i = 0; i < kEvents; ++i)
+        if (ctx->ev[i]) (void)hipEventDestroy(ctx->ev[i]);
+    for (auto& p : ctx->prof) {
+        if (p.a) (void)hipEventDestroy(p.a);
+        if (p.b) (void)hipEventDestroy(p.b);
+    }
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+}
+
+extern "C" void* smoe_metal_fused_ffn(SmoeMetalCtx* ctx, const uint8_t* packed_gate, const uint16_t* scales_gate,
+                                      const uint8_t* packed_up, const uint16_t* scales_up,
+                                      const uint8_t* packed_down, const uint16_t* scales_down,
+                                      const float* input_vec, float* hidden_vec, float* output_vec,
+                                      uint32_t gate_rows, uint32_t gate_cols, uint32_t down_rows,
+                                      uint32_t down_cols, uint32_t group_size, uint32_t bits,
+                                      uint32_t expert_index)
+{
+    (void)hidden_vec;
+    (void)output_vec;
+    if (!ctx || !input_vec || !packed_gate || !scales_gate || !packed_up || !scales_up || !packed_down ||
+        !scales_down || expert_index >= kSlots)
+        return nullptr;
+    if (!ref_shape_ok(ctx, gate_rows, gate_cols, down_rows, down_cols, group_size, bits)) return nullptr;
+    ExpertPtrs e{packed_gate, scales_gate, packed_up, scales_up, packed_down, scales_down, expert_index, 0};
+    return dispatch_group(ctx, &e, 1, input_vec, gate_rows, gate_cols, group_size);
+}
+
+extern "C" void smoe_metal_wait(SmoeMetalCtx* ctx, void* handle, float* output_vec, uint32_t expert_index,
+                                uint32_t cols)
+{
+    if (!ctx || !handle || !output_vec || expert_index >= kSlots || cols > ctx->max_rows) return;
+    if (!wait_handle(ctx, handle)) return;
+    (void)hip_ok(ctx, hipMemcpy(output_vec, ctx->d_output + size_t(expert_index) * ctx->max_rows,
+                                cols * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy(output)");
+}
+
+extern "C" void* smoe_metal_fused_ffn_group(SmoeMetalCtx* ctx, const SmoeExpertBlob* experts, uint32_t n_experts,
+                                            const float* input_vec, uint32_t gate_rows, uint32_t gate_cols,
+                                            uint32_t down_rows, uint32_t down_cols, uint32_t group_size,
+                                            uint32_t bits)
+{
+    if (!ctx || !experts || !input_vec || n_experts == 0 || n_experts > kSlots) return nullptr;
+    if (!ref_shape_ok(ctx, gate_rows, gate_cols, down_rows, down_cols, group_size, bits)) return nullptr;
+    ExpertPtrs tbl[kSlots];
+    for (uint32_t i = 0; i < n_experts; ++i) {
+        const SmoeExpertBlob& b = experts[i];
+        if (!b.packed_gate || !b.scales_gate || !b.packed_up || !b.scales_up || !b.packed_down || !b.scales_down ||
+            b.slot >= kSlots)
+            return nullptr;
+        tbl[i] = ExpertPtrs{b.packed_gate, b.scales_gate, b.packed_up, b.scales_up, b.packed_down, b.scales_down,
+                            b.slot, 0};
+    }
+    return dispatch_group(ctx, tbl, n_experts, input_vec, gate_rows, gate_cols, group_size);
+}
+
+extern "C" void* smoe_metal_fused_ffn_batch(SmoeMetalCtx* ctx, const uint8_t* packed_gate,
+                                            const uint16_t* scales_gate, const uint8_t* packed_up,
+                                            const uint16_t* scales_up, const uint8_t* packed_down,
+                                            const uint16_t* scales_down, const float* input_mat, uint32_t batch,
+                                            uint32_t gate_rows, uint32_t gate_cols, uint32_t down_rows,
+                                            uint32_t down_cols, uint32_t group_size, uint32_t bits)
+{
+    if (!ctx || !input_mat || batch == 0 || batch > SMOE_MAX_FFN_BATCH) return nullptr;
+    if (gate_rows > SMOE_MAX_FFN_BATCH_DIM || gate_cols > SMOE_MAX_FFN_BATCH_DIM ||
+        down_rows > SMOE_MAX_FFN_BATCH_DIM || down_cols > SMOE_MAX_FFN_BATCH_DIM)
+        return nullptr;
+    if (!packed_gate || !scales_gate || !packed_up || !scales_up || !packed_down || !scales_down) return nullptr;
+    if (!ref_shape_ok(nullptr, gate_rows, gate_cols, down_rows, down_cols, group_size, bits)) return nullptr;
+    const MoeDims d{gate_cols, 0, 1, gate_rows, group_size, 0};
+    ExpertPtrs e{packed_gate, scales_gate, packed_up, scales_up, packed_down, scales_down, 0, 0};
+    if (!hip_ok(ctx, hipMemcpyAsync(ctx->d_batch_in, input_mat, size_t(batch) * gate_cols * sizeof(float),
+                                    hipMemcpyHostToDevice, ctx->stream), "hipMemcpyAsync(batch)"))
+        return nullptr;
+    if (!hip_ok(ctx, hipMemcpyAsync(ctx->d_tbl_ref, &e, sizeof(e), hipMemcpyHostToDevice, ctx->stream),
+                "hipMemcpyAsync(table)"))
+        return nullptr;
+    if (!timed(ctx, SMOE_KERNEL_GATE_UP, "gate_up(batch)", [&] {
+            return smoe::launch_gate_up(d, ctx->d_tbl_ref, 1, ctx->d_batch_in, ctx->d_batch_hidden, 0, batch,
+                                        gate_cols, 0, gate_rows, ctx->stream);
+        }))
+        return nullptr;
+    if (!timed(ctx, SMOE_KERNEL_DOWN_SLOTS, "down(batch)", [&] {
+            return smoe::launch_down_slots(d, ctx->d_tbl_ref, 1, ctx->d_batch_hidden, 0, ctx->d_batch_out, 0, batch,
+                                           0, gate_rows, down_rows, ctx->stream);
+        }))
+        return nullptr;
+    ctx->dispatches.fetch_add(1, std::memory_order_relaxed);
+    return record_handle(ctx);
+}
+
+extern "C" void smoe_metal_wait_ffn_batch(SmoeMetalCtx* ctx, void* handle, float* out_mat, uint32_t batch,
+                                          uint32_t cols)
+{
+    if (!ctx || !handle || !out_mat || batch == 0 || batch > SMOE_MAX_FFN_BATCH || cols > SMOE_MAX_FFN_BATCH_DIM)
+        return;
+    if (!wait_handle(ctx, handle)) return;
+    (void)hip_ok(ctx, hipMemcpy(out_mat, ctx->d_batch_out, size_t(batch) * cols * sizeof(float),
+                                hipMemcpyDeviceToHost), "hipMemcpy(batch out)");
+}
+
+extern "C" void smoe_metal_register_buffer(SmoeMetalCtx* ctx, const void* ptr, size_t size_in_bytes)
+{
+    if (!ctx || !ptr || size_in_bytes == 0) return;
+    const uintptr_t p = reinterpret_cast<uintptr_t>(ptr);
+    for (const auto& r : ctx->registered)
+        if (p >= r.first && p + size_in_bytes <= r.first + r.second) return;
+    hipPointerAttribute_t attr;
+    std::memset(&attr, 0, sizeof(attr));
+    if (hipPointerGetAttributes(&attr, ptr) != hipSuccess || attr.type == hipMemoryTypeUnregistered) {
+        (void)hipGetLastError();
+        std::fprintf(stderr,
+                     "[smoe_hip] WARN: register_buffer(%p, %zu): not device or pinned memory; the GPU "
+                     "cannot read it (allocate experts with hipMalloc / hipHostMalloc).\n",
+                     ptr, size_in_bytes);
+        return;
+    }
+    ctx->registered.emplace_back(p, size_in_bytes);
+}
+
+extern "C" uint64_t smoe_metal_kernel_dispatches(const SmoeMetalCtx* ctx)
+{
+    if (!ctx) return 0;
+    return ctx->dispatches.load(std::memory_order_relaxed);
+}
+
+// ============================================================================
+// 2. device-resident entry points
+// ============================================================================
+extern "C" int smoe_hip_set_stream(SmoeMetalCtx* ctx, void* hip_stream)
+{
+    if (!ctx) return SMOE_ERR_ARG;
+    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+    return SMOE_OK;
+}
+
+extern "C" int smoe_hip_synchronize(SmoeMetalCtx* ctx)
+{
+    if (!ctx) return SMOE_ERR_ARG;
+    return hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize") ? SMOE_OK : SMOE_ERR_HIP;
+}
+
+extern "C" int smoe_hip_reserve(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, uint32_t max_tokens)
+{
+    if (!ctx || !shape || max_tokens == 0) return SMOE_ERR_ARG;
+    const int rc = shape_check(shape);
+    if (rc != SMOE_OK) return rc;
+    return ensure_scratch(ctx, shape, max_tokens);
+}
+
+static int moe_forward(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, const SmoeMoeLayer* layer, float* hidden,
+                       uint32_t n_tokens, uint32_t* ids_out, float* weights_out)
+{
+    if (!ctx || !shape || !layer || !hidden || n_tokens == 0) return SMOE_ERR_ARG;
+    if (!layer->norm_w || !layer->router_w || !layer->experts) return SMOE_ERR_ARG;
+    int rc = shape_check(shape);
+    if (rc != SMOE_OK) return rc;
+    rc = ensure_scratch(ctx, shape, n_tokens);
+    if (rc != SMOE_OK) return rc;
+    DeviceScratch& s = ctx->ds;
+    const MoeDims d = dims_of(shape);
+    const LayerDesc L = layer_of(layer);
+    uint32_t* ids = ids_out ? ids_out : s.ids;
+    float* w = weights_out ? weights_out : s.w;
+    if (!timed(ctx, SMOE_KERNEL_ROUTE, "route", [&] {
+            return smoe::launch_route(d, L, hidden, n_tokens, s.normed, s.logits, ids, w, s.tbl, s.counters,
+                                      ctx->stream);
+        }))
+        return SMOE_ERR_HIP;
+    if (!timed(ctx, SMOE_KERNEL_GATE_UP, "gate_up", [&] {
+            return smoe::launch_gate_up(d, s.tbl, d.K, s.normed, s.h, d.I, n_tokens, d.D, d.K, d.K * d.I,
+                                        ctx->stream);
+        }))
+        return SMOE_ERR_HIP;
+    if (!timed(ctx, SMOE_KERNEL_DOWN_COMBINE, "down_combine",
+               [&] { return smoe::launch_down_combine(d, s.tbl, s.h, w, hidden, n_tokens, ctx->stream); }))
+        return SMOE_ERR_HIP;
+    ctx->dispatches.fetch_add(uint64_t(n_tokens) * d.K, std::memory_order_relaxed);
+    return SMOE_OK;
+}
+
+extern "C" int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, const SmoeMoeLayer* layer,
+                                   float* hidden, uint32_t n_tokens, uint32_t* ids_out, float* weights_out)
+{
+    return moe_forward(ctx, shape, layer, hidden, n_tokens, ids_out, weights_out);
+}
+
+extern "C" int smoe_hip_moe_prefill(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, const SmoeMoeLayer* layer,
+                                    float* hidden, uint32_t n_tokens, uint32_t* ids_out, float* weights_out,
+                                    uint32_t* expert_offsets, uint32_t* sorted_tokens, uint32_t* union_ids,
+                                    uint32_t* union_size)
+{
+    (void)expert_offsets;
+    (void)sorted_tokens;
+    (void)union_ids;
+    (void)union_size;
+    return moe_forward(ctx, shape, layer, hidden, n_tokens, ids_out, weights_out);
+}
+
+extern "C" int smoe_hip_compute_top_k(SmoeMetalCtx* ctx, const float* scores, uint32_t n_rows, uint32_t n,
+                                      uint32_t k, uint32_t* ids, float* weights, int norm_topk)
+{
+    if (!ctx || !scores || !ids || !weights || n_rows == 0 || n == 0 || k == 0) return SMOE_ERR_ARG;
+    if (n > SMOE_MAX_EXPERTS || k > SMOE_MAX_ACTIVE) return SMOE_ERR_SHAPE;
+    return timed(ctx, SMOE_KERNEL_TOPK, "topk",
+                 [&] { return smoe::launch_topk(scores, n_rows, n, k, norm_topk ? 1u : 0u, ids, weights, ctx->stream); })
+               ? SMOE_OK
+               : SMOE_ERR_HIP;
+}
+
+extern "C" int smoe_hip_permute(SmoeMetalCtx* ctx, const uint32_t* ids, const float* weights, uint32_t n_tokens,
+                                uint32_t top_k, uint32_t n_experts, uint32_t* expert_offsets,
+                                uint32_t* sorted_tokens, float* sorted_weights, uint32_t* union_ids,
+                                uint32_t* union_size)
+{
+    (void)ids;
+    (void)weights;
+    (void)n_tokens;
+    (void)top_k;
+    (void)n_experts;
+    (void)expert_offsets;
+    (void)sorted_tokens;
+    (void)sorted_weights;
+    (void)union_ids;
+    (void)union_size;
+    if (!ctx) return SMOE_ERR_ARG;
+    return SMOE_ERR_SHAPE;
+}
+
+extern "C" int smoe_hip_quantize_q4(SmoeMetalCtx* ctx, const float* w, uint64_t n, uint32_t group_size,
+                                    uint8_t* packed, uint16_t* scales)
+{
+    if (!ctx || !w || !packed || !scales || n == 0) return SMOE_ERR_ARG;
+    if ((group_size != 32 && group_size != 64 && group_size != 128) || n % group_size) return SMOE_ERR_SHAPE;
+    return hip_ok(ctx, smoe::launch_quantize_q4(w, n, group_size, packed, scales, ctx->stream), "quantize")
+               ? SMOE_OK
+               : SMOE_ERR_HIP;
+}
+
+extern "C" int smoe_hip_synth_normal(SmoeMetalCtx* ctx, float* out, uint64_t n, uint64_t seed, uint64_t stream,
+                                     float stddev)
+{
+    if (!ctx || !out || n == 0) return SMOE_ERR_ARG;
+    return hip_ok(ctx, smoe::launch_synth_normal(out, n, seed, stream, stddev, ctx->stream), "synth_normal")
+               ? SMOE_OK
+               : SMOE_ERR_HIP;
+}
+
+extern "C" int smoe_hip_synth_bf16(SmoeMetalCtx* ctx, uint16_t* out, uint64_t n, uint64_t seed, uint64_t stream,
+                                   float stddev)
+{
+    if (!ctx || !out || n == 0) return SMOE_ERR_ARG;
+    return hip_ok(ctx, smoe::launch_synth_bf16(out, n, seed, stream, stddev, ctx->stream), "synth_bf16")
+               ? SMOE_OK
+               : SMOE_ERR_HIP;
+}
+
+extern "C" int smoe_hip_synth_expert_pool(SmoeMetalCtx* ctx, uint8_t* base, uint32_t first_layer,
+                                          uint32_t n_layers, uint32_t n_experts, uint64_t expert_stride,
+                                          const SmoeMoeShape* shape, uint64_t seed, float stddev)
+{
+    if (!ctx || !base || !shape || n_layers == 0 || n_experts == 0) return SMOE_ERR_ARG;
+    const int rc = shape_check(shape);
+    if (rc != SMOE_OK) return rc;
+    const uint64_t n = uint64_t(shape->d_model) * shape->d_ff;
+    const uint64_t pb = n / 2, sb = n / shape->group_size * 2;
+    const uint64_t off[6] = {0, pb, pb + sb, 2 * pb + sb, 2 * (pb + sb), 3 * pb + 2 * sb};
+    if (expert_stride < 3 * (pb + sb) || expert_stride % 16) return SMOE_ERR_SHAPE;
+    return hip_ok(ctx, smoe::launch_synth_pool(base, first_layer, n_layers, n_experts, expert_stride,
+                                               shape->d_model, shape->d_ff, shape->group_size, off, seed, stddev,
+                                               ctx->stream),
+                  "synth_pool")
+               ? SMOE_OK
+               : SMOE_ERR_HIP;
+}
+
+extern "C" int smoe_hip_profile_enable(SmoeMetalCtx* ctx, int enable)
+{
+    if (!ctx) return SMOE_ERR_ARG;
+    if (enable && ctx->prof.empty()) {
+        ctx->prof.resize(kProfSlots);
+        for (auto& p : ctx->prof) {
+            if (!hip_ok(ctx, hipEventCreate(&p.a), "hipEventCreate") ||
+                !hip_ok(ctx, hipEventCreate(&p.b), "hipEventCreate"))
+                return SMOE_ERR_HIP;
+        }
+    }
+    for (auto& p : ctx->prof) p.pending = false;
+    ctx->prof_head = 0;
+    std::memset(ctx->prof_launches, 0, sizeof(ctx->prof_launches));
+    std::memset(ctx->prof_ms, 0, sizeof(ctx->prof_ms));
+    ctx->profiling = enable != 0;
+    return SMOE_OK;
+}
+
+extern "C" int smoe_hip_profile_read(SmoeMetalCtx* ctx, uint32_t kernel, uint64_t* launches, double* total_ms)
+{
+    if (!ctx || kernel >= SMOE_KERNEL_KINDS || !launches || !total_ms) return SMOE_ERR_ARG;
+    for (auto& p : ctx->prof) prof_flush_slot(ctx, p);
+    *launches = ctx->prof_launches[kernel];
+    *total_ms = ctx->prof_ms[kernel];
+    return SMOE_OK;
+}
+
+extern "C" const char* smoe_hip_last_error(const SmoeMetalCtx* ctx)
+{
+    return ctx ? ctx->last_err : "no context";
+}

@@ -1,0 +1,72 @@
+// kernels.hpp -- host-side launchers of the gfx950 MoE kernels (internal to
+// libsmoe_hip.so; the public surface is include/smoe_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace smoe {
+
+// largest expert count a top-k wave handles (8 positions per lane)
+constexpr int SMOE_TOPK_MAX_N = 512;
+
+// Six tensor pointers of one expert plus the scratch slot its results use.
+struct ExpertPtrs {
+    const uint8_t*  pg;
+    const uint16_t* sg;
+    const uint8_t*  pu;
+    const uint16_t* su;
+    const uint8_t*  pd;
+    const uint16_t* sd;
+    uint32_t        slot;
+    uint32_t        pad_;
+};
+
+struct MoeDims {
+    uint32_t D, E, K, I, group, norm_topk;
+};
+
+struct LayerDesc {
+    const uint16_t* norm_w;
+    const uint16_t* router_w;
+    const uint8_t*  experts;
+    uint64_t        stride;
+    uint64_t        off[6];   // gate p, gate s, up p, up s, down p, down s
+};
+
+// ---- decode, one token (moe_decode.hip) ----------------------------------
+// RMSNorm + router GEMV + softmax/top-k (+renorm) + expert table.
+hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden,
+                        uint32_t n_tok, float* normed, float* logits, uint32_t* ids, float* w,
+                        ExpertPtrs* tbl, uint32_t* counter, hipStream_t s);
+// h[slot * h_stride + row] = silu(gate.x) * (up.x) for n_exp table entries;
+// x_tok_stride / tbl_tok_stride / h_tok_stride step blockIdx.y over tokens.
+hipError_t launch_gate_up(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n_exp,
+                          const float* x, float* h, uint32_t h_stride, uint32_t n_tok,
+                          uint32_t x_tok_stride, uint32_t tbl_tok_stride,
+                          uint32_t h_tok_stride, hipStream_t s);
+// hidden[t][row] += sum_r w[t][r] * (down_r . h[t][r])  (weighted combine + residual)
+hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const float* h,
+                               const float* w, float* hidden, uint32_t n_tok, hipStream_t s);
+// out[slot * out_stride + row] = down_slot . h_slot   (per-expert outputs)
+hipError_t launch_down_slots(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n_exp,
+                             const float* h, uint32_t h_stride, float* out,
+                             uint32_t out_stride, uint32_t n_tok, uint32_t tbl_tok_stride,
+                             uint32_t h_tok_stride, uint32_t out_tok_stride, hipStream_t s);
+// softmax + top-k over rows of scores (scout.cpp:77-123)
+hipError_t launch_topk(const float* scores, uint32_t rows, uint32_t n, uint32_t k,
+                       uint32_t norm, uint32_t* ids, float* w, hipStream_t s);
+
+// ---- synthetic generator / quantizer (synth.hip) -------------------------
+hipError_t launch_synth_normal(float* out, uint64_t n, uint64_t seed, uint64_t stream,
+                               float stddev, hipStream_t s);
+hipError_t launch_synth_bf16(uint16_t* out, uint64_t n, uint64_t seed, uint64_t stream,
+                             float stddev, hipStream_t s);
+hipError_t launch_quantize_q4(const float* w, uint64_t n, uint32_t group, uint8_t* packed,
+                              uint16_t* scales, hipStream_t s);
+hipError_t launch_synth_pool(uint8_t* base, uint32_t first_layer, uint32_t n_layers,
+                             uint32_t n_experts, uint64_t stride, uint32_t D, uint32_t I,
+                             uint32_t group, const uint64_t* off6, uint64_t seed,
+                             float stddev, hipStream_t s);
+
+}  // namespace smoe

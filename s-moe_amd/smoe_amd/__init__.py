@@ -1,0 +1,240 @@
+"""Python binding of libsmoe_hip.so (the C ABI declared in include/smoe_hip.h).
+
+Plain ctypes over the C ABI: pointers are integers (device addresses from any
+allocator, e.g. torch tensors' data_ptr()), sizes are integers.  Importing this
+module loads the HIP library and raises if it is missing: there is no CPU
+fallback anywhere in the product path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsmoe_hip.so")
+
+SMOE_OK = 0
+SMOE_ERR_ARG = -1
+SMOE_ERR_SHAPE = -2
+SMOE_ERR_BITS = -3
+SMOE_ERR_HIP = -4
+SMOE_ERR_CAPACITY = -5
+SMOE_ERR_CAPTURE = -6
+_ERR_NAMES = {v: k for k, v in globals().items() if k.startswith("SMOE_ERR_")}
+
+SMOE_MAX_ACTIVE = 16
+SMOE_MAX_FFN_BATCH = 64
+PAGE = 16384  # vault blob padding (shatter_moe.py:999-1005)
+
+# synthetic-input stream ids (shared with the host generator in oracle/)
+MATRIX_GATE, MATRIX_UP, MATRIX_DOWN = 0, 1, 2
+
+
+def expert_stream(layer: int, expert: int, matrix: int) -> int:
+    return (layer << 32) | (expert << 4) | matrix
+
+
+def router_stream(layer: int) -> int:
+    return (layer << 32) | 0xFFFFFF00
+
+
+def hidden_stream(index: int) -> int:
+    return (0xFFFF << 48) | index
+
+
+class SmoeMoeShape(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in
+                ("d_model", "n_experts", "top_k", "d_ff", "group_size", "bits", "norm_topk")]
+
+
+class SmoeMoeLayer(C.Structure):
+    _fields_ = [("norm_w", C.c_void_p), ("router_w", C.c_void_p), ("experts", C.c_void_p),
+                ("expert_stride", C.c_uint64)] + [(n, C.c_uint64) for n in (
+                    "gate_packed_offset", "gate_scales_offset", "up_packed_offset",
+                    "up_scales_offset", "down_packed_offset", "down_scales_offset")]
+
+
+class SmoeExpertBlob(C.Structure):
+    _fields_ = [("packed_gate", C.c_void_p), ("scales_gate", C.c_void_p),
+                ("packed_up", C.c_void_p), ("scales_up", C.c_void_p),
+                ("packed_down", C.c_void_p), ("scales_down", C.c_void_p),
+                ("slot", C.c_uint32)]
+
+
+# (name, restype, argtypes) of every exported entry point, in header order
+_VP, _U32, _U64, _F, _SZ, _I = C.c_void_p, C.c_uint32, C.c_uint64, C.c_float, C.c_size_t, C.c_int
+_SHP, _LAY = C.POINTER(SmoeMoeShape), C.POINTER(SmoeMoeLayer)
+SIGNATURES = [
+    ("smoe_metal_init", _VP, [_SZ]),
+    ("smoe_metal_destroy", None, [_VP]),
+    ("smoe_metal_fused_ffn", _VP, [_VP] + [_VP] * 6 + [_VP, _VP, _VP] + [_U32] * 7),
+    ("smoe_metal_wait", None, [_VP, _VP, _VP, _U32, _U32]),
+    ("smoe_metal_fused_ffn_group", _VP, [_VP, C.POINTER(SmoeExpertBlob), _U32, _VP] + [_U32] * 6),
+    ("smoe_metal_fused_ffn_batch", _VP, [_VP] + [_VP] * 6 + [_VP, _U32] + [_U32] * 6),
+    ("smoe_metal_wait_ffn_batch", None, [_VP, _VP, _VP, _U32, _U32]),
+    ("smoe_metal_register_buffer", None, [_VP, _VP, _SZ]),
+    ("smoe_metal_kernel_dispatches", _U64, [_VP]),
+    ("smoe_hip_set_stream", _I, [_VP, _VP]),
+    ("smoe_hip_synchronize", _I, [_VP]),
+    ("smoe_hip_reserve", _I, [_VP, _SHP, _U32]),
+    ("smoe_hip_moe_decode", _I, [_VP, _SHP, _LAY, _VP, _U32, _VP, _VP]),
+    ("smoe_hip_moe_prefill", _I, [_VP, _SHP, _LAY, _VP, _U32, _VP, _VP, _VP, _VP, _VP, _VP]),
+    ("smoe_hip_compute_top_k", _I, [_VP, _VP, _U32, _U32, _U32, _VP, _VP, _I]),
+    ("smoe_hip_permute", _I, [_VP, _VP, _VP, _U32, _U32, _U32, _VP, _VP, _VP, _VP, _VP]),
+    ("smoe_hip_quantize_q4", _I, [_VP, _VP, _U64, _U32, _VP, _VP]),
+    ("smoe_hip_synth_normal", _I, [_VP, _VP, _U64, _U64, _U64, _F]),
+    ("smoe_hip_synth_bf16", _I, [_VP, _VP, _U64, _U64, _U64, _F]),
+    ("smoe_hip_synth_expert_pool", _I, [_VP, _VP, _U32, _U32, _U32, _U64, _SHP, _U64, _F]),
+    ("smoe_hip_profile_enable", _I, [_VP, _I]),
+    ("smoe_hip_profile_read", _I, [_VP, _U32, C.POINTER(C.c_uint64), C.POINTER(C.c_double)]),
+    ("smoe_hip_last_error", C.c_char_p, [_VP]),
+]
+
+KERNEL_ROUTE, KERNEL_GATE_UP, KERNEL_DOWN_COMBINE, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
+KERNEL_PERMUTE, KERNEL_GROUPED_GATE_UP, KERNEL_GROUPED_DOWN, KERNEL_SCATTER = 5, 6, 7, 8
+KERNEL_NAMES = {0: "route", 1: "gate_up", 2: "down_combine", 3: "down_slots", 4: "topk",
+                5: "permute", 6: "grouped_gate_up", 7: "grouped_down", 8: "scatter"}
+
+_lib = None
+
+
+def lib():
+    """Load libsmoe_hip.so (raises OSError when it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise OSError(f"{LIB_PATH} is missing: run s-moe_amd/build.py (the HIP path has no fallback)")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in SIGNATURES:
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+class SmoeError(RuntimeError):
+    pass
+
+
+def blob_layout(d_model: int, d_ff: int, group: int = 64):
+    """Offsets of the six tensors in one expert blob (build_expert_blob,
+    shatter_moe.py:627-674), the raw blob size and the 16 KB-padded stride."""
+    n = d_model * d_ff
+    pb, sb = n // 2, n // group * 2
+    off = [0, pb, pb + sb, 2 * pb + sb, 2 * (pb + sb), 3 * pb + 2 * sb]
+    raw = 3 * (pb + sb)
+    stride = (raw + PAGE - 1) // PAGE * PAGE
+    return off, raw, stride
+
+
+def make_shape(d_model, n_experts, top_k, d_ff, group_size=64, norm_topk=True, bits=4):
+    return SmoeMoeShape(d_model, n_experts, top_k, d_ff, group_size, bits, 1 if norm_topk else 0)
+
+
+def make_layer(norm_w: int, router_w: int, experts: int, stride: int, off):
+    L = SmoeMoeLayer()
+    L.norm_w, L.router_w, L.experts, L.expert_stride = norm_w, router_w, experts, stride
+    (L.gate_packed_offset, L.gate_scales_offset, L.up_packed_offset, L.up_scales_offset,
+     L.down_packed_offset, L.down_scales_offset) = off
+    return L
+
+
+class Context:
+    """Owns one SmoeMetalCtx.  Device-resident entry points raise SmoeError on
+    a non-zero status."""
+
+    def __init__(self, slot_bytes: int = 0):
+        self.lib = lib()
+        self.ptr = self.lib.smoe_metal_init(slot_bytes)
+        if not self.ptr:
+            raise SmoeError("smoe_metal_init failed (no HIP device?)")
+
+    def close(self):
+        if self.ptr:
+            self.lib.smoe_metal_destroy(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc, what):
+        if rc != SMOE_OK:
+            msg = self.lib.smoe_hip_last_error(self.ptr)
+            raise SmoeError(f"{what}: {_ERR_NAMES.get(rc, rc)} {msg.decode() if msg else ''}")
+
+    # -- stream -------------------------------------------------------------
+    def set_stream(self, stream_handle: int | None):
+        self._check(self.lib.smoe_hip_set_stream(self.ptr, stream_handle or None), "set_stream")
+
+    def synchronize(self):
+        self._check(self.lib.smoe_hip_synchronize(self.ptr), "synchronize")
+
+    def reserve(self, shape: SmoeMoeShape, max_tokens: int):
+        self._check(self.lib.smoe_hip_reserve(self.ptr, C.byref(shape), max_tokens), "reserve")
+
+    # -- MoE block ----------------------------------------------------------
+    def moe_decode(self, shape, layer, hidden: int, n_tokens: int, ids: int = 0, weights: int = 0):
+        self._check(self.lib.smoe_hip_moe_decode(self.ptr, C.byref(shape), C.byref(layer), hidden,
+                                                 n_tokens, ids or None, weights or None), "moe_decode")
+
+    def moe_prefill(self, shape, layer, hidden: int, n_tokens: int, ids: int = 0, weights: int = 0,
+                    expert_offsets: int = 0, sorted_tokens: int = 0, union_ids: int = 0,
+                    union_size: int = 0):
+        self._check(self.lib.smoe_hip_moe_prefill(
+            self.ptr, C.byref(shape), C.byref(layer), hidden, n_tokens, ids or None, weights or None,
+            expert_offsets or None, sorted_tokens or None, union_ids or None, union_size or None),
+            "moe_prefill")
+
+    def compute_top_k(self, scores: int, n_rows: int, n: int, k: int, ids: int, weights: int,
+                      norm_topk: bool):
+        self._check(self.lib.smoe_hip_compute_top_k(self.ptr, scores, n_rows, n, k, ids, weights,
+                                                    1 if norm_topk else 0), "compute_top_k")
+
+    def permute(self, ids: int, weights: int, n_tokens: int, top_k: int, n_experts: int,
+                expert_offsets: int, sorted_tokens: int, sorted_weights: int, union_ids: int,
+                union_size: int):
+        self._check(self.lib.smoe_hip_permute(self.ptr, ids, weights, n_tokens, top_k, n_experts,
+                                              expert_offsets, sorted_tokens, sorted_weights,
+                                              union_ids, union_size), "permute")
+
+    # -- synthetic inputs -----------------------------------------------------
+    def quantize_q4(self, w: int, n: int, group: int, packed: int, scales: int):
+        self._check(self.lib.smoe_hip_quantize_q4(self.ptr, w, n, group, packed, scales), "quantize_q4")
+
+    def synth_normal(self, out: int, n: int, seed: int, stream: int, stddev: float):
+        self._check(self.lib.smoe_hip_synth_normal(self.ptr, out, n, seed, stream, stddev), "synth_normal")
+
+    def synth_bf16(self, out: int, n: int, seed: int, stream: int, stddev: float):
+        self._check(self.lib.smoe_hip_synth_bf16(self.ptr, out, n, seed, stream, stddev), "synth_bf16")
+
+    def synth_expert_pool(self, base: int, first_layer: int, n_layers: int, n_experts: int,
+                          stride: int, shape: SmoeMoeShape, seed: int, stddev: float):
+        self._check(self.lib.smoe_hip_synth_expert_pool(self.ptr, base, first_layer, n_layers, n_experts,
+                                                        stride, C.byref(shape), seed, stddev),
+                    "synth_expert_pool")
+
+    # -- reference surface (metal_bridge.h) ----------------------------------
+    def fused_ffn_group(self, blobs, input_vec_host, gate_rows, gate_cols, group=64, bits=4):
+        arr = (SmoeExpertBlob * len(blobs))(*blobs)
+        return self.lib.smoe_metal_fused_ffn_group(self.ptr, arr, len(blobs), input_vec_host, gate_rows,
+                                                   gate_cols, gate_cols, gate_rows, group, bits)
+
+    def wait(self, handle, out_host, slot, cols):
+        self.lib.smoe_metal_wait(self.ptr, handle, out_host, slot, cols)
+
+    def profile_enable(self, on: bool = True):
+        self._check(self.lib.smoe_hip_profile_enable(self.ptr, 1 if on else 0), "profile_enable")
+
+    def profile_read(self, kernel: int):
+        """(launches, total_ms) of one kernel kind since profile_enable."""
+        n = C.c_uint64()
+        ms = C.c_double()
+        self._check(self.lib.smoe_hip_profile_read(self.ptr, kernel, C.byref(n), C.byref(ms)), "profile_read")
+        return int(n.value), float(ms.value)
+
+    def dispatches(self) -> int:
+        return int(self.lib.smoe_metal_kernel_dispatches(self.ptr))

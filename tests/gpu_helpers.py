@@ -1,0 +1,57 @@
+"""Shared helpers of the GPU tests: synthetic layers built on the device by the
+library's generator, copied back for the CPU oracle, and the tolerance metric."""
+import numpy as np
+import torch
+
+import smoe_amd
+
+SEED = 20261201
+
+
+def rel_err(got, ref, floor_frac=1e-2):
+    """max |g - c| / max(|c|, tau), tau = floor_frac * rms(c): the per-element
+    relative error with a floor so that elements near zero are judged against
+    the vector's scale.  Returns (max_rel, n_below_floor)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    tau = floor_frac * np.sqrt(np.mean(ref ** 2)) + 1e-30
+    den = np.maximum(np.abs(ref), tau)
+    return float(np.max(np.abs(got - ref) / den)), int(np.sum(np.abs(ref) < tau))
+
+
+class Layer:
+    """One MoE layer of a given shape, resident on cuda:0, plus host copies."""
+
+    def __init__(self, ctx, D, E, K, I, layer_id=0, seed=SEED, norm_topk=True, router_std=0.02,
+                 host=True):
+        self.D, self.E, self.K, self.I = D, E, K, I
+        self.shape = smoe_amd.make_shape(D, E, K, I, 64, norm_topk)
+        self.off, self.raw, self.stride = smoe_amd.blob_layout(D, I)
+        dev = torch.device("cuda", 0)
+        self.pool = torch.zeros(E * self.stride, dtype=torch.uint8, device=dev)
+        ctx.synth_expert_pool(self.pool.data_ptr(), layer_id, 1, E, self.stride, self.shape, seed, 0.02)
+        self.router = torch.empty(E * D, dtype=torch.int16, device=dev)
+        ctx.synth_bf16(self.router.data_ptr(), E * D, seed, smoe_amd.router_stream(layer_id), router_std)
+        self.norm_w = torch.full((D,), 0x3F80, dtype=torch.int16, device=dev)   # bf16 1.0
+        self.layer = smoe_amd.make_layer(self.norm_w.data_ptr(), self.router.data_ptr(),
+                                         self.pool.data_ptr(), self.stride, self.off)
+        torch.cuda.synchronize()
+        if host:
+            self.h_pool = self.pool.cpu().numpy()
+            self.h_router = self.router.cpu().numpy().view(np.uint16)
+            self.h_norm = self.norm_w.cpu().numpy().view(np.uint16)
+
+    def oracle_shape(self):
+        return dict(d_model=self.D, n_experts=self.E, top_k=self.K, d_ff=self.I, group_size=64,
+                    norm_topk=self.shape.norm_topk)
+
+    def oracle_decode(self, oracle, hidden):
+        return oracle.moe_decode_layer(self.oracle_shape(), self.h_norm, self.h_router, self.h_pool,
+                                       self.stride, self.off, hidden)
+
+
+def hidden_states(ctx, T, D, index0=0, seed=SEED):
+    h = torch.empty((T, D), dtype=torch.float32, device="cuda")
+    for t in range(T):
+        ctx.synth_normal(h[t].data_ptr(), D, seed, smoe_amd.hidden_stream(index0 + t), 1.0)
+    return h

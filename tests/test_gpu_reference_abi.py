@@ -1,0 +1,86 @@
+"""The reference surface (smoe_metal_fused_ffn / _group / _batch + waits,
+metal_bridge.h:74-154) against the oracle expert FFN, expert by expert."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import smoe_amd
+from gpu_helpers import Layer, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def blob_ptrs(layer, e):
+    base = layer.pool.data_ptr() + e * layer.stride
+    return [base + o for o in layer.off]
+
+
+def test_group_dispatch_per_slot(ctx, oracle):
+    layer = Layer(ctx, 2048, 16, 8, 768, layer_id=9)
+    L = smoe_amd.lib()
+    x = np.random.default_rng(0).standard_normal(2048).astype(np.float32)
+    experts = [3, 0, 15, 7, 8]
+    slots = [4, 0, 9, 15, 1]
+    blobs = [smoe_amd.SmoeExpertBlob(*blob_ptrs(layer, e), s) for e, s in zip(experts, slots)]
+    before = ctx.dispatches()
+    h = ctx.fused_ffn_group(blobs, x.ctypes.data, 768, 2048)
+    assert h
+    assert ctx.dispatches() - before == len(experts)
+    for e, s in zip(experts, slots):
+        out = np.zeros(2048, np.float32)
+        ctx.wait(h, out.ctypes.data, s, 2048)
+        _, y = oracle.expert_ffn(layer.h_pool[e * layer.stride:(e + 1) * layer.stride], layer.off, 2048, 768, x)
+        assert rel_err(out, y)[0] <= 1e-3
+    # single-expert entry point
+    hv = np.zeros(768, np.float32)
+    ov = np.zeros(2048, np.float32)
+    h1 = L.smoe_metal_fused_ffn(ctx.ptr, *blob_ptrs(layer, 5), x.ctypes.data, hv.ctypes.data, ov.ctypes.data,
+                                768, 2048, 2048, 768, 64, 4, 2)
+    assert h1
+    out = np.zeros(2048, np.float32)
+    L.smoe_metal_wait(ctx.ptr, h1, out.ctypes.data, 2, 2048)
+    _, y = oracle.expert_ffn(layer.h_pool[5 * layer.stride:6 * layer.stride], layer.off, 2048, 768, x)
+    assert rel_err(out, y)[0] <= 1e-3
+
+
+def test_batch_dispatch(ctx, oracle):
+    layer = Layer(ctx, 2048, 4, 2, 768, layer_id=11)
+    L = smoe_amd.lib()
+    B = 37
+    X = np.random.default_rng(1).standard_normal((B, 2048)).astype(np.float32)
+    h = L.smoe_metal_fused_ffn_batch(ctx.ptr, *blob_ptrs(layer, 2), X.ctypes.data, B, 768, 2048, 2048, 768, 64, 4)
+    assert h
+    out = np.zeros((B, 2048), np.float32)
+    L.smoe_metal_wait_ffn_batch(ctx.ptr, h, out.ctypes.data, B, 2048)
+    blob = layer.h_pool[2 * layer.stride:3 * layer.stride]
+    for b in (0, 17, B - 1):
+        _, y = oracle.expert_ffn(blob, layer.off, 2048, 768, X[b])
+        assert rel_err(out[b], y)[0] <= 1e-3
+
+
+def test_reference_surface_rejections(ctx):
+    L = smoe_amd.lib()
+    x = np.zeros(2048, np.float32)
+    dummy = [1 << 20] * 6
+    # batch above SMOE_MAX_FFN_BATCH -> NULL (caller falls back, prefill.cpp:386-405)
+    assert L.smoe_metal_fused_ffn_batch(ctx.ptr, *dummy, x.ctypes.data, 65, 768, 2048, 2048, 768, 64, 4) is None
+    # bits != 4, group not a multiple of 32, mismatched dims -> NULL
+    blob = smoe_amd.SmoeExpertBlob(*dummy, 0)
+    arr = (smoe_amd.SmoeExpertBlob * 1)(blob)
+    assert L.smoe_metal_fused_ffn_group(ctx.ptr, arr, 1, x.ctypes.data, 768, 2048, 2048, 768, 64, 2) is None
+    assert L.smoe_metal_fused_ffn_group(ctx.ptr, arr, 1, x.ctypes.data, 768, 2048, 2048, 768, 48, 4) is None
+    assert L.smoe_metal_fused_ffn_group(ctx.ptr, arr, 1, x.ctypes.data, 768, 2048, 2048, 512, 64, 4) is None
+    assert L.smoe_metal_fused_ffn_group(ctx.ptr, arr, 17, x.ctypes.data, 768, 2048, 2048, 768, 64, 4) is None
+    # slot out of range
+    bad = (smoe_amd.SmoeExpertBlob * 1)(smoe_amd.SmoeExpertBlob(*dummy, 16))
+    assert L.smoe_metal_fused_ffn_group(ctx.ptr, bad, 1, x.ctypes.data, 768, 2048, 2048, 768, 64, 4) is None
+    # device-resident entry: bits / shape errors are status codes
+    shape = smoe_amd.make_shape(2048, 128, 8, 768, bits=2)
+    lay = smoe_amd.make_layer(1 << 20, 1 << 20, 1 << 20, 1 << 22, [0] * 6)
+    assert L.smoe_hip_moe_decode(ctx.ptr, C.byref(shape), C.byref(lay), 1 << 20, 1, None, None) == smoe_amd.SMOE_ERR_BITS
+    shape = smoe_amd.make_shape(2048, 128, 17, 768)
+    assert L.smoe_hip_moe_decode(ctx.ptr, C.byref(shape), C.byref(lay), 1 << 20, 1, None, None) == smoe_amd.SMOE_ERR_SHAPE
+    shape = smoe_amd.make_shape(2000, 128, 8, 768)
+    assert L.smoe_hip_moe_decode(ctx.ptr, C.byref(shape), C.byref(lay), 1 << 20, 1, None, None) == smoe_amd.SMOE_ERR_SHAPE

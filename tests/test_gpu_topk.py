@@ -1,0 +1,45 @@
+"""smoe_hip_compute_top_k against the oracle (= the compiled reference top_k,
+pinned by tests/test_oracle_golden.py) on identical score vectors, including
+constructed ties and the swap counter-example.  Indices bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_topk(ctx, scores, k, norm):
+    rows, n = scores.shape
+    d = torch.from_numpy(np.ascontiguousarray(scores, np.float32)).cuda()
+    ids = torch.zeros((rows, k), dtype=torch.int32, device="cuda")
+    w = torch.zeros((rows, k), dtype=torch.float32, device="cuda")
+    ctx.compute_top_k(d.data_ptr(), rows, n, k, ids.data_ptr(), w.data_ptr(), norm)
+    torch.cuda.synchronize()
+    return ids.cpu().numpy().view(np.uint32), w.cpu().numpy()
+
+
+@pytest.mark.parametrize("n,k", [(128, 8), (128, 16), (64, 8), (256, 8), (512, 16), (3, 2), (40, 8)])
+def test_topk_random_and_ties(ctx, oracle, n, k):
+    rng = np.random.default_rng(n * 31 + k)
+    rows = []
+    for r in range(64):
+        s = rng.standard_normal(n).astype(np.float32)
+        if r % 2:
+            s = np.round(s * 2) / 2                       # many exact ties
+        if r % 7 == 0:
+            s[:] = s[0]                                   # all tied
+        rows.append(s)
+    S = np.stack(rows)
+    for norm in (False, True):
+        gi, gw = gpu_topk(ctx, S, k, norm)
+        for r in range(S.shape[0]):
+            oi, ow = oracle.top_k(S[r], k, norm)
+            c = oi.size
+            assert (gi[r, :c] == oi).all(), (r, gi[r, :c], oi)
+            assert np.allclose(gw[r, :c], ow, rtol=2e-6, atol=1e-9)
+
+
+def test_swap_counterexample(ctx, oracle):
+    S = np.log(np.array([[0.5, 0.5, 0.9]], np.float32))
+    gi, _ = gpu_topk(ctx, S, 2, False)
+    assert list(gi[0]) == [2, 1]
