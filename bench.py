@@ -210,13 +210,14 @@ def cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, n_la
         ctx.moe_decode(shape, lay, gpu_h.data_ptr(), 1, ids.data_ptr())
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        out, oid, ow, *_ = O.moe_decode_layer(oshape, h_norm, h_router, h_pool, stride, off, h)
+        out, oid, ow, _lg, _nr, yo = O.moe_decode_layer(oshape, h_norm, h_router, h_pool, stride, off, h)
         total += time.perf_counter() - t0
         g = gpu_h.cpu().numpy()
         id_mismatch += int((ids.cpu().numpy().view(np.uint32) != oid).sum())
-        dref = out.astype(np.float64) - h
+        dref = (ow.astype(np.float64)[:, None] * yo.astype(np.float64)).sum(0)
         tau = 1e-2 * np.sqrt(np.mean(dref ** 2))
-        worst = max(worst, float(np.max(np.abs((g - h) - dref) / np.maximum(np.abs(dref), tau))))
+        diff = np.maximum(np.abs((g.astype(np.float64) - h) - dref) - np.spacing(np.abs(g)), 0.0)
+        worst = max(worst, float(np.max(diff / np.maximum(np.abs(dref), tau))))
         h = out
     return {
         "value": round(1.0 / total * (n_layers / c["layers"]), 4) if total > 0 else None,

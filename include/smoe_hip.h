@@ -158,8 +158,9 @@ typedef struct {
     uint64_t down_packed_offset, down_scales_offset;
 } SmoeMoeLayer;
 
-/* Use `hip_stream` (a hipStream_t) for all later work of this context; NULL
- * selects the context's own stream.  No synchronisation is implied. */
+/* Use `hip_stream` (a hipStream_t, NULL = the null stream) for all later work
+ * of this context.  Until it is called, the context uses a non-blocking stream
+ * of its own.  No synchronisation is implied. */
 int smoe_hip_set_stream(SmoeMetalCtx* ctx, void* hip_stream);
 
 /* Synchronise the context's stream. */

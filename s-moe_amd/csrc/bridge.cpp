@@ -327,7 +327,7 @@ extern "C" SmoeMetalCtx* smoe_metal_init(size_t slot_bytes)
 extern "C" void smoe_metal_destroy(SmoeMetalCtx* ctx)
 {
     if (!ctx) return;
-    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamSynchronize(ctx->stream);
     if (ctx->own_stream && ctx->own_stream != ctx->stream) (void)hipStreamSynchronize(ctx->own_stream);
     free_device_scratch(ctx->ds);
     dfree(ctx->d_input);
@@ -469,7 +469,7 @@ extern "C" uint64_t smoe_metal_kernel_dispatches(const SmoeMetalCtx* ctx)
 extern "C" int smoe_hip_set_stream(SmoeMetalCtx* ctx, void* hip_stream)
 {
     if (!ctx) return SMOE_ERR_ARG;
-    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+    ctx->stream = static_cast<hipStream_t>(hip_stream);
     return SMOE_OK;
 }
 

@@ -77,12 +77,28 @@ __device__ __forceinline__ float det_cos2pi(float t)
     return sign * c;
 }
 
+// Correctly rounded square root for x > 0: v_sqrt_f32 is within 1 ulp; the
+// fma residuals x - s_dn*s and x - s_up*s tell on which side of the midpoints
+// to the neighbouring floats the exact root lies.
+__device__ __forceinline__ float sqrt_rn(float x)
+{
+    if (!(x > 0.0f)) return __builtin_sqrtf(x);
+    float s = __builtin_amdgcn_sqrtf(x);
+    const float s_dn = __uint_as_float(__float_as_uint(s) - 1u);
+    const float s_up = __uint_as_float(__float_as_uint(s) + 1u);
+    const float r_dn = __builtin_fmaf(-s_dn, s, x);
+    const float r_up = __builtin_fmaf(-s_up, s, x);
+    if (r_dn <= 0.0f) s = s_dn;
+    if (r_up > 0.0f) s = s_up;
+    return s;
+}
+
 __device__ __forceinline__ float det_normal(uint64_t key, uint64_t i)
 {
     const uint64_t h = fmix64(key + (i + 1) * GAMMA);
     const float u1 = static_cast<float>(static_cast<uint32_t>((h >> 40) + 1u)) * 5.9604644775390625e-8f;
     const float u2 = static_cast<float>(static_cast<uint32_t>((h >> 16) & 0xFFFFFFu)) * 5.9604644775390625e-8f;
-    const float r = __fsqrt_rn(-2.0f * det_log(u1));
+    const float r = sqrt_rn(-2.0f * det_log(u1));
     return r * det_cos2pi(u2);
 }
 

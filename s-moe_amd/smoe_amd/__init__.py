@@ -168,6 +168,7 @@ class Context:
 
     # -- stream -------------------------------------------------------------
     def set_stream(self, stream_handle: int | None):
+        """Launch on this hipStream_t from now on (0 / None = the null stream)."""
         self._check(self.lib.smoe_hip_set_stream(self.ptr, stream_handle or None), "set_stream")
 
     def synchronize(self):

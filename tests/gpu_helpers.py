@@ -8,15 +8,31 @@ import smoe_amd
 SEED = 20261201
 
 
-def rel_err(got, ref, floor_frac=1e-2):
-    """max |g - c| / max(|c|, tau), tau = floor_frac * rms(c): the per-element
-    relative error with a floor so that elements near zero are judged against
-    the vector's scale.  Returns (max_rel, n_below_floor)."""
+def rel_err(got, ref, floor_frac=1e-2, slack=None):
+    """max (|g - c| - slack) / max(|c|, tau), tau = floor_frac * rms(c): the
+    per-element relative error with a floor so that elements near zero are
+    judged against the vector's scale.  `slack` (absolute, per element)
+    discounts a rounding both sides share by construction, e.g. the fp32
+    residual add when a delta is read back as hidden_out - hidden_in.
+    Returns (max_rel, n_below_floor)."""
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     tau = floor_frac * np.sqrt(np.mean(ref ** 2)) + 1e-30
     den = np.maximum(np.abs(ref), tau)
-    return float(np.max(np.abs(got - ref) / den)), int(np.sum(np.abs(ref) < tau))
+    diff = np.abs(got - ref)
+    if slack is not None:
+        diff = np.maximum(diff - np.asarray(slack, np.float64), 0.0)
+    return float(np.max(diff / den)), int(np.sum(np.abs(ref) < tau))
+
+
+def moe_delta_err(got_hidden, h0, expert_out, weights):
+    """Relative error of the GPU's MoE delta (hidden_out - hidden_in) against
+    the oracle's sum_r w_r * y_r, with one ulp of hidden_out as slack for the
+    fp32 residual add (decode.cpp:506-509) that both sides round."""
+    got_hidden = np.asarray(got_hidden, np.float32)
+    ref = (np.asarray(weights, np.float64)[:, None] * np.asarray(expert_out, np.float64)).sum(0)
+    delta = got_hidden.astype(np.float64) - np.asarray(h0, np.float64)
+    return rel_err(delta, ref, slack=np.spacing(np.abs(got_hidden)))
 
 
 class Layer:

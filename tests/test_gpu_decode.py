@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import Layer, hidden_states, rel_err
+from gpu_helpers import Layer, hidden_states, moe_delta_err, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -26,9 +26,7 @@ def run_and_check(ctx, oracle, layer, T=1, index0=0):
         out, oid, ow, logits, normed, yo = layer.oracle_decode(oracle, h0[t])
         assert (gids[t] == oid).all(), (t, gids[t], oid)
         assert np.allclose(gw[t], ow, rtol=1e-5, atol=1e-7)
-        delta_ref = out.astype(np.float64) - h0[t]
-        delta_got = got[t].astype(np.float64) - h0[t]
-        e1, _ = rel_err(delta_got, delta_ref)
+        e1, _ = moe_delta_err(got[t], h0[t], yo, ow)
         e2, _ = rel_err(got[t], out)
         worst = max(worst, e1, e2)
         # routing margin between rank k-1 and rank k (reported, not asserted)

@@ -36,7 +36,8 @@ def test_topk_random_and_ties(ctx, oracle, n, k):
             oi, ow = oracle.top_k(S[r], k, norm)
             c = oi.size
             assert (gi[r, :c] == oi).all(), (r, gi[r, :c], oi)
-            assert np.allclose(gw[r, :c], ow, rtol=2e-6, atol=1e-9)
+            # softmax sums differ in order (parallel vs sequential) and exp implementation
+            assert np.allclose(gw[r, :c], ow, rtol=1e-5, atol=1e-9)
 
 
 def test_swap_counterexample(ctx, oracle):
