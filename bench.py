@@ -41,9 +41,10 @@ def kernel_bytes(c):
     D, E, K, I = c["D"], c["E"], c["K"], c["I"]
     mat = D * I // 2 + D * I // 64 * 2            # packed nibbles + fp16 scales of one matrix
     return {
-        "route": E * D * 2 + D * 2 + D * 4 + D * 4,        # router bf16 + norm w + hidden in + normed out
-        "gate_up": K * 2 * mat + D * 4 + K * I * 4,         # 8 experts' gate+up, x in, h out
-        "down_combine": K * mat + K * I * 4 + K * 4 + 2 * D * 4,   # 8 experts' down, h in, hidden r/w
+        # router bf16 + norm weights + hidden in + 8 experts' gate+up + h out
+        "moe_up": E * D * 2 + D * 2 + D * 4 + K * 2 * mat + K * I * 4,
+        # 8 experts' down + h in + weights + hidden read and written
+        "moe_down": K * mat + K * I * 4 + K * 4 + 2 * D * 4,
     }
 
 
@@ -137,8 +138,7 @@ def main():
     torch.cuda.synchronize()
     kb = kernel_bytes(c)
     kern = {}
-    for kid, name in ((smoe_amd.KERNEL_ROUTE, "route"), (smoe_amd.KERNEL_GATE_UP, "gate_up"),
-                      (smoe_amd.KERNEL_DOWN_COMBINE, "down_combine")):
+    for kid, name in ((smoe_amd.KERNEL_MOE_UP, "moe_up"), (smoe_amd.KERNEL_MOE_DOWN, "moe_down")):
         n, ms = ctx.profile_read(kid)
         if n:
             avg_us = ms * 1e3 / n
@@ -146,8 +146,8 @@ def main():
                               gbs=round(kb[name] / (avg_us * 1e-6) / 1e9, 1))
     ctx.profile_enable(False)
     dom = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches"])
-    expert_bytes = kb["gate_up"] + kb["down_combine"]
-    expert_us = kern["gate_up"]["avg_us"] + kern["down_combine"]["avg_us"]
+    layer_bytes = kb["moe_up"] + kb["moe_down"]
+    layer_us = kern["moe_up"]["avg_us"] + kern["moe_down"]["avg_us"]
     roofline = {
         "bound": "hbm", "kernel": dom,
         "achieved": kern[dom]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -171,7 +171,7 @@ def main():
                    "resident_expert_bytes": NL * E * raw},
         "roofline": roofline,
         "kernels": kern,
-        "expert_ffn_gbs": round(expert_bytes / (expert_us * 1e-6) / 1e9, 1),
+        "layer_kernels_gbs": round(layer_bytes / (layer_us * 1e-6) / 1e9, 1),
         "layer_gbs_in_stack": round((sum(kb.values())) * NL * tok_s / 1e9, 1),
         "cpu_baseline": cpu,
     }

@@ -139,7 +139,7 @@ typedef struct {
     uint32_t n_experts;   /* experts per layer E      (128)         */
     uint32_t top_k;       /* routed experts per token (8), <= 16    */
     uint32_t d_ff;        /* expert intermediate I    (768 / 1536)  */
-    uint32_t group_size;  /* SMOE quant group         (64)          */
+    uint32_t group_size;  /* SMOE quant group: must be 64 (vault format) */
     uint32_t bits;        /* must be 4                              */
     uint32_t norm_topk;   /* renormalise the k weights (Qwen3: 1)   */
 } SmoeMoeShape;
@@ -163,7 +163,8 @@ typedef struct {
  * of its own.  No synchronisation is implied. */
 int smoe_hip_set_stream(SmoeMetalCtx* ctx, void* hip_stream);
 
-/* Synchronise the context's stream. */
+/* Synchronise the context's stream; also reports (SMOE_ERR_HIP) a timed-out
+ * routing exchange inside smoe_hip_moe_decode. */
 int smoe_hip_synchronize(SmoeMetalCtx* ctx);
 
 /* Reserve device scratch for layers of this shape and up to max_tokens tokens
@@ -238,9 +239,9 @@ int smoe_hip_synth_expert_pool(SmoeMetalCtx* ctx, uint8_t* base, uint32_t first_
  * When enabled, every kernel the context launches outside graph capture is
  * bracketed by HIP events on the stream it runs on; profile_read returns the
  * launch count and summed event time of one kernel kind. */
-#define SMOE_KERNEL_ROUTE         0   /* RMSNorm + router GEMV + top-k        */
-#define SMOE_KERNEL_GATE_UP       1   /* gate/up GEMV + SiLU, all k experts   */
-#define SMOE_KERNEL_DOWN_COMBINE  2   /* down GEMV + weighted combine + residual */
+#define SMOE_KERNEL_MOE_UP        0   /* RMSNorm + router + top-k + gate/up GEMV + SiLU */
+#define SMOE_KERNEL_GATE_UP       1   /* gate/up GEMV + SiLU (reference surface)        */
+#define SMOE_KERNEL_MOE_DOWN      2   /* down GEMV + weighted combine + residual        */
 #define SMOE_KERNEL_DOWN_SLOTS    3   /* down GEMV, per-slot outputs          */
 #define SMOE_KERNEL_TOPK          4
 #define SMOE_KERNEL_PERMUTE       5

@@ -5,7 +5,7 @@
 // device-resident entry points.  The context owns one HIP stream (or uses the
 // caller's), pre-allocated scratch, and a ring of events backing the
 // monotonically increasing handles of the reference (metal_bridge.mm:423-429).
-#include "../../include/smoe_hip.h"
+#include "smoe_hip.h"
 
 #include <hip/hip_runtime.h>
 
@@ -29,12 +29,11 @@ constexpr uint32_t kEvents = 256;              // handle ring
 struct DeviceScratch {
     // capacities
     uint32_t D = 0, E = 0, K = 0, I = 0, T = 0;
-    float* normed = nullptr;     // [T x D]
-    float* logits = nullptr;     // [T x E]
+    uint64_t* ll = nullptr;      // [T x (E+1)] routing exchange words
+    uint32_t* err = nullptr;     // [1] device-side error flags
     uint32_t* ids = nullptr;     // [T x K]
     float* w = nullptr;          // [T x K]
     ExpertPtrs* tbl = nullptr;   // [T x K]
-    uint32_t* counters = nullptr;// [T]
     float* h = nullptr;          // [T x K x I]
 };
 
@@ -105,12 +104,11 @@ void dfree(T*& p)
 
 void free_device_scratch(DeviceScratch& s)
 {
-    dfree(s.normed);
-    dfree(s.logits);
+    dfree(s.ll);
+    dfree(s.err);
     dfree(s.ids);
     dfree(s.w);
     dfree(s.tbl);
-    dfree(s.counters);
     dfree(s.h);
     s = DeviceScratch{};
 }
@@ -138,6 +136,7 @@ int shape_check(const SmoeMoeShape* s)
     if (s->d_model == 0 || s->d_ff == 0 || s->n_experts == 0 || s->top_k == 0) return SMOE_ERR_SHAPE;
     if (s->d_model % 64 || s->d_ff % 64 || s->d_model % g || s->d_ff % g) return SMOE_ERR_SHAPE;
     if (s->d_model > SMOE_MAX_DIM || s->d_ff > SMOE_MAX_DIM) return SMOE_ERR_SHAPE;
+    if (g != 64) return SMOE_ERR_SHAPE;   // the vault format's group (shatter_moe.py Q2_GROUP_SIZE)
     if (s->top_k > SMOE_MAX_ACTIVE || s->top_k > s->n_experts) return SMOE_ERR_SHAPE;
     if (s->n_experts > SMOE_MAX_EXPERTS) return SMOE_ERR_SHAPE;
     if (static_cast<uint64_t>(s->top_k) * (s->d_ff / 32) > 8ull * 64 * 4) return SMOE_ERR_SHAPE;
@@ -175,7 +174,7 @@ bool stream_capturing(hipStream_t s)
 int ensure_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
 {
     DeviceScratch& c = ctx->ds;
-    if (c.normed && c.D >= s->d_model && c.E >= s->n_experts && c.K >= s->top_k && c.I >= s->d_ff && c.T >= T)
+    if (c.ll && c.D >= s->d_model && c.E >= s->n_experts && c.K >= s->top_k && c.I >= s->d_ff && c.T >= T)
         return SMOE_OK;
     if (stream_capturing(ctx->stream)) return SMOE_ERR_CAPTURE;
     if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
@@ -187,15 +186,12 @@ int ensure_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
     n.T = std::max(c.T, T);
     free_device_scratch(c);
     const size_t T_ = n.T;
-    bool ok = dalloc(ctx, &n.normed, T_ * n.D) && dalloc(ctx, &n.logits, T_ * n.E) &&
-              dalloc(ctx, &n.ids, T_ * n.K) && dalloc(ctx, &n.w, T_ * n.K) && dalloc(ctx, &n.tbl, T_ * n.K) &&
-              dalloc(ctx, &n.counters, T_) && dalloc(ctx, &n.h, T_ * n.K * n.I);
+    bool ok = dalloc(ctx, &n.ll, T_ * (n.E + 1)) && dalloc(ctx, &n.err, 1) && dalloc(ctx, &n.ids, T_ * n.K) &&
+              dalloc(ctx, &n.w, T_ * n.K) && dalloc(ctx, &n.tbl, T_ * n.K) && dalloc(ctx, &n.h, T_ * n.K * n.I);
+    // the exchange words start disarmed; every launch pair leaves them so
+    ok = ok && hip_ok(ctx, hipMemset(n.ll, 0, T_ * (n.E + 1) * sizeof(uint64_t)), "hipMemset") &&
+         hip_ok(ctx, hipMemset(n.err, 0, sizeof(uint32_t)), "hipMemset");
     if (!ok) {
-        free_device_scratch(n);
-        return SMOE_ERR_HIP;
-    }
-    // counters start at zero; every k_route launch leaves them at zero again
-    if (!hip_ok(ctx, hipMemset(n.counters, 0, T_ * sizeof(uint32_t)), "hipMemset")) {
         free_device_scratch(n);
         return SMOE_ERR_HIP;
     }
@@ -476,7 +472,17 @@ extern "C" int smoe_hip_set_stream(SmoeMetalCtx* ctx, void* hip_stream)
 extern "C" int smoe_hip_synchronize(SmoeMetalCtx* ctx)
 {
     if (!ctx) return SMOE_ERR_ARG;
-    return hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize") ? SMOE_OK : SMOE_ERR_HIP;
+    if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
+    if (ctx->ds.err) {
+        uint32_t e = 0;
+        if (!hip_ok(ctx, hipMemcpy(&e, ctx->ds.err, sizeof(e), hipMemcpyDeviceToHost), "hipMemcpy(err)"))
+            return SMOE_ERR_HIP;
+        if (e) {
+            std::snprintf(ctx->last_err, sizeof(ctx->last_err), "device: routing exchange timed out (flags %u)", e);
+            return SMOE_ERR_HIP;
+        }
+    }
+    return SMOE_OK;
 }
 
 extern "C" int smoe_hip_reserve(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, uint32_t max_tokens)
@@ -501,18 +507,12 @@ static int moe_forward(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, const SmoeM
     const LayerDesc L = layer_of(layer);
     uint32_t* ids = ids_out ? ids_out : s.ids;
     float* w = weights_out ? weights_out : s.w;
-    if (!timed(ctx, SMOE_KERNEL_ROUTE, "route", [&] {
-            return smoe::launch_route(d, L, hidden, n_tokens, s.normed, s.logits, ids, w, s.tbl, s.counters,
-                                      ctx->stream);
+    if (!timed(ctx, SMOE_KERNEL_MOE_UP, "moe_up", [&] {
+            return smoe::launch_moe_up(d, L, hidden, n_tokens, s.ll, s.h, ids, w, s.tbl, s.err, ctx->stream);
         }))
         return SMOE_ERR_HIP;
-    if (!timed(ctx, SMOE_KERNEL_GATE_UP, "gate_up", [&] {
-            return smoe::launch_gate_up(d, s.tbl, d.K, s.normed, s.h, d.I, n_tokens, d.D, d.K, d.K * d.I,
-                                        ctx->stream);
-        }))
-        return SMOE_ERR_HIP;
-    if (!timed(ctx, SMOE_KERNEL_DOWN_COMBINE, "down_combine",
-               [&] { return smoe::launch_down_combine(d, s.tbl, s.h, w, hidden, n_tokens, ctx->stream); }))
+    if (!timed(ctx, SMOE_KERNEL_MOE_DOWN, "moe_down",
+               [&] { return smoe::launch_down_combine(d, s.tbl, s.h, w, hidden, s.ll, n_tokens, ctx->stream); }))
         return SMOE_ERR_HIP;
     ctx->dispatches.fetch_add(uint64_t(n_tokens) * d.K, std::memory_order_relaxed);
     return SMOE_OK;

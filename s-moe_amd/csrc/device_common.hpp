@@ -149,6 +149,95 @@ __device__ __forceinline__ float q4_chunk_dot(uint4 v, const float* __restrict__
     return (a0 + a1) + (a2 + a3);
 }
 
+// ---------------------------------------------------------------------------
+// Integer form of a 32-value activation chunk for 4-bit dot products.
+// The chunk is scaled by 2^sh (sh = 22 - exponent of its absmax) and rounded
+// to integers t_k, |t_k| <= 2^22; each t_k is written in six balanced hex
+// digits d_l in [-8, 7] (t = sum_l 16^l d_l), stored as two's-complement
+// nibbles in the weights' nibble order (nibble k of dword w = element 8w+k).
+// Then sum_k (c_k - 8) t_k = sum_l 16^l sum_k (c_k - 8) d_lk is 6 v_dot8 per
+// dword of codes, exact in int32 (|sum| <= 32 * 8 * 2^22 = 2^30), and
+//   sum_k (c_k - 7.5) a_k / 7.5 = (sum_k (c_k - 8) t_k + X / 2) * 2^-sh / 7.5
+// with X = sum_k t_k.  The rounding of a_k to t_k is at most 2^-22 of the
+// chunk's absmax, the level of fp32 accumulation error.
+// ---------------------------------------------------------------------------
+constexpr int Q4_DIGITS = 6;
+
+struct Q4Act {
+    uint32_t dig[Q4_DIGITS][4];   // [digit l][dword w]
+    float xsum_half;              // X / 2
+    float kscale;                 // 2^-sh / 7.5
+};
+
+__device__ __forceinline__ void q4_act_from_floats(const float (&a)[32], Q4Act& q)
+{
+    float amax = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(a[k]));
+    // amax < 2^e  ->  |a * 2^(22-e)| < 2^22
+    const int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
+    const int sh = 22 - e;
+    // v = a * 2^sh + 1.5 * 2^23 lies in [2^23, 2^24] with spacing 1, so the
+    // add rounds to nearest-even integer and bits(v) - bits(1.5 * 2^23) = t;
+    // u = t + B with B = 0x888888 has the unsigned digits d_l + 8 and
+    // u ^ B their two's-complement nibbles
+    constexpr float kMagic = 12582912.0f;               // 1.5 * 2^23, bits 0x4B400000
+    constexpr uint32_t kB = 0x888888u;
+    uint32_t y[32];
+    uint32_t usum = 0;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        const float v = __builtin_ldexpf(a[k], sh) + kMagic;
+        const uint32_t u = __float_as_uint(v) + (kB - 0x4B400000u);
+        usum += u;
+        y[k] = u ^ kB;
+    }
+    q.xsum_half = 0.5f * static_cast<float>(static_cast<int>(usum - 32u * kB));
+    q.kscale = __builtin_ldexpf(1.0f / 7.5f, -sh);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t* t = y + 8 * w;
+        // byte b of the even (odd) elements of this dword, in element order
+        const uint32_t ea = __builtin_amdgcn_perm(t[2], t[0], 0x05010400u);   // t0.0 t2.0 t0.1 t2.1
+        const uint32_t eb = __builtin_amdgcn_perm(t[6], t[4], 0x05010400u);   // t4.0 t6.0 t4.1 t6.1
+        const uint32_t ec = __builtin_amdgcn_perm(t[2], t[0], 0x0C0C0602u);   // t0.2 t2.2
+        const uint32_t ed = __builtin_amdgcn_perm(t[6], t[4], 0x0C0C0602u);   // t4.2 t6.2
+        const uint32_t oa = __builtin_amdgcn_perm(t[3], t[1], 0x05010400u);
+        const uint32_t ob = __builtin_amdgcn_perm(t[7], t[5], 0x05010400u);
+        const uint32_t oc = __builtin_amdgcn_perm(t[3], t[1], 0x0C0C0602u);
+        const uint32_t od = __builtin_amdgcn_perm(t[7], t[5], 0x0C0C0602u);
+        const uint32_t E[3] = {__builtin_amdgcn_perm(eb, ea, 0x05040100u), __builtin_amdgcn_perm(eb, ea, 0x07060302u),
+                               __builtin_amdgcn_perm(ed, ec, 0x05040100u)};
+        const uint32_t O[3] = {__builtin_amdgcn_perm(ob, oa, 0x05040100u), __builtin_amdgcn_perm(ob, oa, 0x07060302u),
+                               __builtin_amdgcn_perm(od, oc, 0x05040100u)};
+#pragma unroll
+        for (int b = 0; b < 3; ++b) {
+            q.dig[2 * b][w] = (E[b] & 0x0F0F0F0Fu) | ((O[b] << 4) & 0xF0F0F0F0u);
+            q.dig[2 * b + 1][w] = ((E[b] >> 4) & 0x0F0F0F0Fu) | (O[b] & 0xF0F0F0F0u);
+        }
+    }
+}
+
+// sum_k (c_k - 7.5) a_k / 7.5 over one 16-byte chunk of codes (before the
+// group scale)
+__device__ __forceinline__ float q4_chunk_dot8(uint4 v, const Q4Act& q)
+{
+    // c ^ 8 per nibble is c - 8 as a two's-complement nibble
+    const uint32_t c[4] = {v.x ^ 0x88888888u, v.y ^ 0x88888888u, v.z ^ 0x88888888u, v.w ^ 0x88888888u};
+    int s[Q4_DIGITS];
+#pragma unroll
+    for (int l = 0; l < Q4_DIGITS; ++l) {
+        s[l] = 0;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            s[l] = __builtin_amdgcn_sdot8(static_cast<int>(c[w]), static_cast<int>(q.dig[l][w]), s[l], false);
+    }
+    uint32_t acc = static_cast<uint32_t>(s[Q4_DIGITS - 1]);
+#pragma unroll
+    for (int l = Q4_DIGITS - 2; l >= 0; --l) acc = acc * 16u + static_cast<uint32_t>(s[l]);
+    return (static_cast<float>(static_cast<int>(acc)) + q.xsum_half) * q.kscale;
+}
+
 // Per-chunk affine epilogue of the dequant w = (c - 7.5) * (1/7.5) * s:
 //   sum_j w_j x_j = s * (sum_j c_j x_j / 7.5 - sum_j x_j)   (kernels.metal:140-145)
 __device__ __forceinline__ float q4_chunk_epilogue(float s, float cx, float xsum)

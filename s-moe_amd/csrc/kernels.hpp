@@ -9,6 +9,7 @@ namespace smoe {
 
 // largest expert count a top-k wave handles (8 positions per lane)
 constexpr int SMOE_TOPK_MAX_N = 512;
+constexpr int SMOE_TOPK_MAX_K = 16;
 
 // Six tensor pointers of one expert plus the scratch slot its results use.
 struct ExpertPtrs {
@@ -35,19 +36,22 @@ struct LayerDesc {
 };
 
 // ---- decode, one token (moe_decode.hip) ----------------------------------
-// RMSNorm + router GEMV + softmax/top-k (+renorm) + expert table.
-hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden,
-                        uint32_t n_tok, float* normed, float* logits, uint32_t* ids, float* w,
-                        ExpertPtrs* tbl, uint32_t* counter, hipStream_t s);
+// Router + softmax/top-k (+renorm) + gate/up/SiLU of the selected experts:
+// h [T x K x I]; publishes ids/w [T x K] and the expert table [T x K].
+// ll [T x (E+1)] must be zero on entry (launch_down_combine re-arms it);
+// err receives 1 if the routing exchange timed out.
+hipError_t launch_moe_up(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t n_tok, uint64_t* ll,
+                         float* h, uint32_t* ids, float* w, ExpertPtrs* tbl, uint32_t* err, hipStream_t s);
 // h[slot * h_stride + row] = silu(gate.x) * (up.x) for n_exp table entries;
 // x_tok_stride / tbl_tok_stride / h_tok_stride step blockIdx.y over tokens.
 hipError_t launch_gate_up(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n_exp,
                           const float* x, float* h, uint32_t h_stride, uint32_t n_tok,
                           uint32_t x_tok_stride, uint32_t tbl_tok_stride,
                           uint32_t h_tok_stride, hipStream_t s);
-// hidden[t][row] += sum_r w[t][r] * (down_r . h[t][r])  (weighted combine + residual)
-hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const float* h,
-                               const float* w, float* hidden, uint32_t n_tok, hipStream_t s);
+// hidden[t][row] += sum_r w[t][r] * (down_r . h[t][r])  (weighted combine + residual);
+// zeroes ll [T x (E+1)] for the next launch_moe_up
+hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const float* h, const float* w,
+                               float* hidden, uint64_t* ll, uint32_t n_tok, hipStream_t s);
 // out[slot * out_stride + row] = down_slot . h_slot   (per-expert outputs)
 hipError_t launch_down_slots(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n_exp,
                              const float* h, uint32_t h_stride, float* out,

@@ -1,11 +1,14 @@
 // moe_decode.hip -- batch-1 decode MoE block on gfx950.
 //
-// Three launches per layer, each sized to fill 256 CUs:
-//   k_route        RMSNorm (common.hpp:245-256) + bf16 router GEMV
-//                  (common.hpp:293-306); the last block to finish runs softmax +
-//                  top-k (scout.cpp:77-123) and the renormalisation
-//                  (decode.cpp:296-302) in one wave and writes the expert table.
-//   k_q4_rows      gate+up+SiLU GEMV of every selected expert in one launch
+// Two launches per layer; the kernel boundary between them is the layer's
+// second global synchronisation point (a launch is cheaper on MI355X than an
+// in-kernel grid barrier):
+//   k_moe_up       RMSNorm (common.hpp:245-256) + bf16 router GEMV
+//                  (common.hpp:293-306) in the first blocks, published as
+//                  flag-carrying 64-bit words that every block polls; softmax +
+//                  top-k (scout.cpp:77-123) with the renormalisation
+//                  (decode.cpp:296-302) block-wide in every block; then the
+//                  gate+up+SiLU GEMV of every selected expert in one launch
 //                  (kernels.metal:240-337): one wave per block of rows, each
 //                  lane owning a fixed 16-byte column chunk of every row, so
 //                  its 32 activations stay in VGPRs and the dequant folds into
@@ -54,42 +57,26 @@ __device__ __forceinline__ uint32_t sel(const uint32_t (&a)[VPL], uint32_t j)
     return r;
 }
 
-// scores: n values (agent-scope loads: written by other blocks of this grid).
-// Lane r < count receives (id_r, w_r); returns count.
+// Load the n scores of one row into the positions of this lane (position
+// p = lane + 64 j); padding positions get -inf.
 template <int VPL>
-__device__ uint32_t topk_wave(const float* scores, uint32_t n, uint32_t k, uint32_t norm,
-                              uint32_t& my_id, float& my_w)
+__device__ __forceinline__ void topk_load(const float* scores, uint32_t n, float (&p)[VPL])
 {
     const int lane = threadIdx.x & (WAVE - 1);
-    float p[VPL];
-    uint32_t id[VPL], key[VPL];
-    float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const uint32_t pos = lane + WAVE * j;
-        p[j] = pos < n ? __hip_atomic_load(scores + pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                       : -INFINITY;
-        id[j] = pos;
-        m = fmaxf(m, p[j]);
+        p[j] = pos < n ? scores[pos] : -INFINITY;
     }
-    m = wave_max(m);
-    float sum = 0.f;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-        const uint32_t pos = lane + WAVE * j;
-        p[j] = pos < n ? expf(p[j] - m) : 0.f;
-        sum += p[j];
-    }
-    sum = wave_sum(sum);
-    const float inv_sum = (sum > 0.f) ? 1.0f / sum : 0.f;
-#pragma unroll
-    for (int j = 0; j < VPL; ++j) {
-        const uint32_t pos = lane + WAVE * j;
-        p[j] *= inv_sum;
-        key[j] = pos < n ? (isnan(p[j]) ? 1u : __float_as_uint(p[j]) + 1u) : 0u;
-    }
+}
 
-    const uint32_t count = k < n ? k : n;
+// k rounds of the swap-based selection sort over keys held in lanes (see
+// above); lane r < count receives (id_r, w_r), renormalised if norm.
+template <int VPL>
+__device__ void topk_select(float (&p)[VPL], uint32_t (&id)[VPL], uint32_t (&key)[VPL], uint32_t count,
+                            uint32_t norm, uint32_t& my_id, float& my_w)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
     float ksum = 0.f;
     my_id = 0;
     my_w = 0.f;
@@ -126,132 +113,351 @@ __device__ uint32_t topk_wave(const float* scores, uint32_t n, uint32_t k, uint3
         if (static_cast<uint32_t>(lane) == s) { my_id = id_b; my_w = val_b; }
     }
     if (norm && ksum > 0.f) my_w = my_w * (1.0f / ksum);
+}
+
+// ---------------------------------------------------------------------------
+// Softmax + top-k of n scores held in one wave (position p = lane + 64 j).
+// Fast path: a radix select over the probability bits finds the m-th largest
+// key (m = count + 1 when count < n), the m candidates are ranked among
+// themselves; when those m probabilities are pairwise distinct (and no
+// probability is NaN) the reference's k rounds of selection with swaps
+// (scout.cpp:101-110) pick exactly ranks 0..count-1.  Any tie falls back to
+// the exact swap emulation topk_select.  Lane r < count receives (id_r, w_r).
+// ---------------------------------------------------------------------------
+template <int VPL>
+__device__ uint32_t topk_fast(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t norm, uint32_t& my_id,
+                              float& my_w)
+{
+    __shared__ uint32_t c_key[SMOE_TOPK_MAX_K + 1];
+    __shared__ uint32_t c_pos[SMOE_TOPK_MAX_K + 1];
+    __shared__ float c_p[SMOE_TOPK_MAX_K + 1];
+    const int lane = threadIdx.x & (WAVE - 1);
+    // softmax (scout.cpp:85-98)
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+        if (lane + WAVE * j < n) m = fmaxf(m, v[j]);
+    m = wave_max(m);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const uint32_t pos = lane + WAVE * j;
+        v[j] = pos < n ? expf(v[j] - m) : 0.f;
+        sum += v[j];
+    }
+    sum = wave_sum(sum);
+    const float inv_sum = (sum > 0.f) ? 1.0f / sum : 0.f;
+    uint32_t key[VPL], id[VPL];
+    bool nan = false;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const uint32_t pos = lane + WAVE * j;
+        v[j] *= inv_sum;
+        id[j] = pos;
+        nan |= pos < n && isnan(v[j]);
+        key[j] = pos < n ? (isnan(v[j]) ? 1u : __float_as_uint(v[j]) + 1u) : 0u;
+    }
+    const uint32_t count = k < n ? k : n;
+    const uint32_t msel = count < n ? count + 1 : count;
+    bool fast = __ballot(nan) == 0;
+    if (fast) {
+        // m-th largest key: keys are at most bits(1.0f) + 1 < 2^30
+        uint32_t T = 0;
+        for (int bit = 29; bit >= 0; --bit) {
+            const uint32_t cand = T | (1u << bit);
+            uint32_t c = 0;
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) c += __popcll(__ballot(key[j] >= cand));
+            if (c >= msel) T = cand;
+        }
+        uint32_t base = 0;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const uint64_t mk = __ballot(key[j] >= T);
+            if (key[j] >= T) {
+                const uint32_t slot = base + __popcll(mk & ((1ull << lane) - 1ull));
+                if (slot <= SMOE_TOPK_MAX_K) {
+                    c_key[slot] = key[j];
+                    c_pos[slot] = id[j];
+                    c_p[slot] = v[j];
+                }
+            }
+            base += __popcll(mk);
+        }
+        fast = base == msel;          // no tie across the boundary
+        if (fast) {
+            __builtin_amdgcn_wave_barrier();
+            uint32_t rank = 0;
+            bool dup = false;
+            const uint32_t kr = static_cast<uint32_t>(lane) < msel ? c_key[lane] : 0u;
+            for (uint32_t q = 0; q < msel; ++q) {
+                const uint32_t kq = c_key[q];
+                rank += kq > kr;
+                dup |= (kq == kr) && (q != static_cast<uint32_t>(lane));
+            }
+            fast = __ballot(static_cast<uint32_t>(lane) < msel && dup) == 0;
+            const uint32_t pr = static_cast<uint32_t>(lane) < msel ? c_pos[lane] : 0u;
+            const float wr = static_cast<uint32_t>(lane) < msel ? c_p[lane] : 0.f;
+            __builtin_amdgcn_wave_barrier();
+            if (fast && static_cast<uint32_t>(lane) < msel) {
+                c_pos[rank] = pr;
+                c_p[rank] = wr;
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (fast) {
+                float ksum = 0.f;
+                for (uint32_t r = 0; r < count; ++r) ksum += c_p[r];   // sequential, as the reference
+                my_id = static_cast<uint32_t>(lane) < count ? c_pos[lane] : 0u;
+                my_w = static_cast<uint32_t>(lane) < count ? c_p[lane] : 0.f;
+                if (norm && ksum > 0.f) my_w = my_w * (1.0f / ksum);
+            }
+        }
+    }
+    if (!fast) topk_select<VPL>(v, id, key, count, norm, my_id, my_w);
     return count;
 }
 
-// positions per lane for n experts: 1, 2, 4 or 8 (n <= 512)
-static inline int topk_vpl(uint32_t n) { return n <= 64 ? 1 : n <= 128 ? 2 : n <= 256 ? 4 : 8; }
+// positions per lane for n experts: 2 (n <= 128) or 8 (n <= 512)
+static inline int topk_vpl(uint32_t n) { return n <= 128 ? 2 : 8; }
 
 // ---------------------------------------------------------------------------
-// k_route
-// ---------------------------------------------------------------------------
-constexpr int ROUTE_WAVES = 4;
-
-template <int VPL>
-__global__ __launch_bounds__(ROUTE_WAVES * WAVE)
-void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden,
-             float* __restrict__ normed_out, float* __restrict__ logits,
-             uint32_t* __restrict__ ids_out, float* __restrict__ w_out,
-             ExpertPtrs* __restrict__ tbl, uint32_t* __restrict__ counter)
-{
-    extern __shared__ float xs[];                  // normed activations [D]
-    __shared__ float red[ROUTE_WAVES];
-    __shared__ int is_last;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const uint32_t D = d.D;
-    const uint32_t tok = blockIdx.y;
-    hidden += static_cast<size_t>(tok) * D;
-    normed_out += static_cast<size_t>(tok) * D;
-    logits += static_cast<size_t>(tok) * d.E;
-    ids_out += static_cast<size_t>(tok) * d.K;
-    w_out += static_cast<size_t>(tok) * d.K;
-    tbl += static_cast<size_t>(tok) * d.K;
-    counter += tok;
-
-    float ss = 0.f;
-    for (uint32_t i = tid * 4; i < D; i += blockDim.x * 4) {
-        const float4 v = *reinterpret_cast<const float4*>(hidden + i);
-        *reinterpret_cast<float4*>(xs + i) = v;
-        ss = fmaf(v.x, v.x, ss);
-        ss = fmaf(v.y, v.y, ss);
-        ss = fmaf(v.z, v.z, ss);
-        ss = fmaf(v.w, v.w, ss);
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) red[wv] = ss;
-    __syncthreads();
-    float tot = 0.f;
-#pragma unroll
-    for (int w = 0; w < ROUTE_WAVES; ++w) tot += red[w];
-    const float inv = 1.0f / sqrtf(tot / static_cast<float>(D) + 1e-6f);
-    for (uint32_t i = tid; i < D; i += blockDim.x) {
-        const float v = (xs[i] * inv) * bf16_to_f32(*gptr(L.norm_w + i));
-        xs[i] = v;
-        if (blockIdx.x == 0) normed_out[i] = v;
-    }
-    __syncthreads();
-
-    const uint32_t row = blockIdx.x * ROUTE_WAVES + wv;
-    if (row < d.E) {
-        const uint16_t* wr = L.router_w + static_cast<size_t>(row) * D;
-        float a0 = 0.f, a1 = 0.f;
-#pragma unroll 4
-        for (uint32_t c = lane * 8; c < D; c += 8 * WAVE) {
-            const uint4 v = load_u4(wr + c);
-            const float4 xa = *reinterpret_cast<const float4*>(xs + c);
-            const float4 xb = *reinterpret_cast<const float4*>(xs + c + 4);
-            a0 = fmaf(bf16_to_f32(v.x & 0xFFFFu), xa.x, a0);
-            a1 = fmaf(bf16_to_f32(v.x >> 16), xa.y, a1);
-            a0 = fmaf(bf16_to_f32(v.y & 0xFFFFu), xa.z, a0);
-            a1 = fmaf(bf16_to_f32(v.y >> 16), xa.w, a1);
-            a0 = fmaf(bf16_to_f32(v.z & 0xFFFFu), xb.x, a0);
-            a1 = fmaf(bf16_to_f32(v.z >> 16), xb.y, a1);
-            a0 = fmaf(bf16_to_f32(v.w & 0xFFFFu), xb.z, a0);
-            a1 = fmaf(bf16_to_f32(v.w >> 16), xb.w, a1);
-        }
-        const float acc = wave_sum(a0 + a1);
-        if (lane == 0) logits[row] = acc;
-    }
-
-    // last block to finish runs the selection for the whole layer
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(counter, 1u);
-        is_last = (prev == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (!is_last || wv != 0) return;
-    __threadfence();
-    uint32_t my_id;
-    float my_w;
-    const uint32_t count = topk_wave<VPL>(logits, d.E, d.K, d.norm_topk, my_id, my_w);
-    if (static_cast<uint32_t>(lane) < count) {
-        ids_out[lane] = my_id;
-        w_out[lane] = my_w;
-        const uint8_t* b = L.experts + static_cast<size_t>(my_id) * L.stride;
-        ExpertPtrs e;
-        e.pg = b + L.off[0];
-        e.sg = reinterpret_cast<const uint16_t*>(b + L.off[1]);
-        e.pu = b + L.off[2];
-        e.su = reinterpret_cast<const uint16_t*>(b + L.off[3]);
-        e.pd = b + L.off[4];
-        e.sd = reinterpret_cast<const uint16_t*>(b + L.off[5]);
-        e.slot = lane;
-        e.pad_ = 0;
-        tbl[lane] = e;
-    }
-    if (lane == 0) *counter = 0;                    // ready for the next launch / replay
-}
-
-// ---------------------------------------------------------------------------
-// k_topk: one wave per row of scores (Scout::compute_top_k)
+// k_topk: Scout::compute_top_k (scout.cpp:718-720) on rows of scores, one
+// wave per row, through the same selection k_moe_up uses.
 // ---------------------------------------------------------------------------
 template <int VPL>
 __global__ __launch_bounds__(WAVE)
-void k_topk(const float* __restrict__ scores, uint32_t n, uint32_t k, uint32_t norm,
-            uint32_t* __restrict__ ids, float* __restrict__ w)
+void k_topk(const float* __restrict__ scores, uint32_t n, uint32_t k, uint32_t norm, uint32_t* __restrict__ ids,
+            float* __restrict__ w)
 {
-    const uint32_t row = blockIdx.x;
+    const size_t row = blockIdx.x;
+    float v[VPL];
+    topk_load<VPL>(scores + row * n, n, v);
     uint32_t my_id;
     float my_w;
-    const float* sr = scores + static_cast<size_t>(row) * n;
-    const uint32_t count = topk_wave<VPL>(sr, n, k, norm, my_id, my_w);
-    const uint32_t lane = threadIdx.x;
-    if (lane < count) {
-        ids[static_cast<size_t>(row) * k + lane] = my_id;
-        w[static_cast<size_t>(row) * k + lane] = my_w;
+    const uint32_t count = topk_fast<VPL>(v, n, k, norm, my_id, my_w);
+    if (threadIdx.x < count) {
+        ids[row * k + threadIdx.x] = my_id;
+        w[row * k + threadIdx.x] = my_w;
     }
+}
+
+// ---------------------------------------------------------------------------
+// k_moe_up: RMSNorm + router + softmax/top-k + gate/up/SiLU for one layer.
+// One wave per block; grid (I / 8, K, T).  Lane l owns the 32 columns of
+// chunk l (+64 j) of the hidden dimension throughout.  Every wave:
+//   1. loads its hidden and norm-weight chunks (block b < E also router row b),
+//   2. RMS-normalises them, normed = (x * inv) * w (common.hpp:245-256),
+//   3. turns the normed chunk into 4-bit digit words (Q4Act),
+//   4. block b < E: logit b = router_w[b] . normed (common.hpp:293-306),
+//      published as a flag-carrying 64-bit word,
+//   5. polls the E logits of its token and selects the experts itself
+//      (softmax + top-k, scout.cpp:77-123; renormalised, decode.cpp:296-302),
+//   6. streams 8 rows of gate and up of the expert of rank blockIdx.y and
+//      writes h = silu(gate) * up (kernels.metal:240-337).
+// Producers have the lowest block ids of their token, so they are dispatched
+// before any consumer that waits on them; a bounded spin reports a timeout
+// (err) instead of hanging.  Block 0 of each token publishes ids, weights
+// and the expert table.  Steps 1-3 overlap the router rows' latency.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t ll_word(float v) { return (1ull << 32) | __float_as_uint(v); }
+
+constexpr uint32_t SPIN_LIMIT = 1u << 22;
+constexpr int UP_RB = 8;   // rows per wave
+constexpr int SMOE_G = 64; // SMOE-Q4 group size (shatter_moe.py Q2_GROUP_SIZE)
+
+template <int CPL, int VPL, bool PRODUCER>
+__device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L, const float* __restrict__ hv,
+                                            uint64_t* __restrict__ ll, float* __restrict__ h,
+                                            uint32_t* __restrict__ ids_out, float* __restrict__ w_out,
+                                            ExpertPtrs* __restrict__ tbl_out, uint32_t* __restrict__ err,
+                                            uint32_t b)
+{
+    constexpr int RB = UP_RB;
+    const int lane = threadIdx.x;
+    const uint32_t tok = blockIdx.z, r = blockIdx.y;
+    const uint32_t D = d.D, nch = D >> 5;
+
+    // 1. chunk loads (router last, so the norm can start before it lands)
+    float4 x[CPL][8];
+    uint4 g[CPL][4], rw[CPL][4];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) x[j][q] = load_f4(hv + c * 32 + q * 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) g[j][q] = load_u4(L.norm_w + c * 32 + q * 8);
+    }
+    if constexpr (PRODUCER) {
+        const uint16_t* wr = L.router_w + static_cast<size_t>(b) * D;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) rw[j][q] = load_stream_u4(wr + c * 32 + q * 8);
+        }
+    }
+    // 2. RMS norm over the wave's D columns
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const bool ok = lane + WAVE * j < nch;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            if (!ok) x[j][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+            ss = fmaf(x[j][q].x, x[j][q].x, ss);
+            ss = fmaf(x[j][q].y, x[j][q].y, ss);
+            ss = fmaf(x[j][q].z, x[j][q].z, ss);
+            ss = fmaf(x[j][q].w, x[j][q].w, ss);
+        }
+    }
+    ss = wave_sum(ss);
+    // rms_norm_bf16 (common.hpp:245-256): inv = 1 / sqrt(ss / n + 1e-6)
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + 1e-6f);
+    float a[CPL][32];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const uint32_t g0 = (q & 1) ? g[j][q >> 1].z : g[j][q >> 1].x;
+            const uint32_t g1 = (q & 1) ? g[j][q >> 1].w : g[j][q >> 1].y;
+            a[j][4 * q + 0] = (x[j][q].x * inv) * bf16_to_f32(g0 & 0xFFFFu);
+            a[j][4 * q + 1] = (x[j][q].y * inv) * bf16_to_f32(g0 >> 16);
+            a[j][4 * q + 2] = (x[j][q].z * inv) * bf16_to_f32(g1 & 0xFFFFu);
+            a[j][4 * q + 3] = (x[j][q].w * inv) * bf16_to_f32(g1 >> 16);
+        }
+    }
+    // 3. digit form of the normed chunk
+    Q4Act qa[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) q4_act_from_floats(a[j], qa[j]);
+    // 4. router rows b, b + nb, ... (nb blocks per token; padding lanes hold normed 0)
+    if constexpr (PRODUCER) {
+        const uint32_t nb = gridDim.x * gridDim.y;
+        for (uint32_t row = b;;) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t w4[4] = {rw[j][q].x, rw[j][q].y, rw[j][q].z, rw[j][q].w};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        acc = fmaf(bf16_to_f32(w4[t] & 0xFFFFu), a[j][8 * q + 2 * t], acc);
+                        acc = fmaf(bf16_to_f32(w4[t] >> 16), a[j][8 * q + 2 * t + 1], acc);
+                    }
+                }
+            }
+            acc = wave_sum(acc);
+            if (lane == 0) __hip_atomic_store(ll + row, ll_word(acc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            row += nb;
+            if (row >= d.E) break;
+            const uint16_t* wr = L.router_w + static_cast<size_t>(row) * D;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) rw[j][q] = load_stream_u4(wr + c * 32 + q * 8);
+            }
+        }
+    }
+    // 5. wait for the E logits, then select
+    float v[VPL];
+    {
+        uint32_t spins = 0;
+        bool all;
+        do {
+            all = true;
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) {
+                const uint32_t pos = lane + WAVE * j;
+                if (pos < d.E) {
+                    const uint64_t w64 = __hip_atomic_load(ll + pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    v[j] = __uint_as_float(static_cast<uint32_t>(w64));
+                    all &= (w64 >> 32) != 0;
+                }
+            }
+            all = __ballot(!all) == 0;
+            if (!all && ++spins > SPIN_LIMIT) {
+                if (lane == 0) atomicOr(err, 1u);
+                break;
+            }
+        } while (!all);
+    }
+    uint32_t my_id;
+    float my_w;
+    topk_fast<VPL>(v, d.E, d.K, d.norm_topk, my_id, my_w);
+    const uint32_t expert = readlane_u32(my_id, r);
+
+    if (b == 0 && static_cast<uint32_t>(lane) < d.K) {
+        const size_t o = static_cast<size_t>(tok) * d.K + lane;
+        ids_out[o] = my_id;
+        w_out[o] = my_w;
+        const uint8_t* bb = L.experts + static_cast<size_t>(my_id) * L.stride;
+        ExpertPtrs e;
+        e.pg = bb + L.off[0];
+        e.sg = reinterpret_cast<const uint16_t*>(bb + L.off[1]);
+        e.pu = bb + L.off[2];
+        e.su = reinterpret_cast<const uint16_t*>(bb + L.off[3]);
+        e.pd = bb + L.off[4];
+        e.sd = reinterpret_cast<const uint16_t*>(bb + L.off[5]);
+        e.slot = lane;
+        e.pad_ = 0;
+        tbl_out[o] = e;
+    }
+
+    // 6. 8 rows of gate and up: every weight load in flight before any is used
+    const uint32_t row0 = blockIdx.x * RB;
+    const uint8_t* blob = L.experts + static_cast<size_t>(expert) * L.stride;
+    const uint8_t* pa = blob + L.off[0];
+    const uint16_t* sa = reinterpret_cast<const uint16_t*>(blob + L.off[1]);
+    const uint8_t* pb = blob + L.off[2];
+    const uint16_t* sb = reinterpret_cast<const uint16_t*>(blob + L.off[3]);
+    const uint32_t row_bytes = D >> 1, row_scales = D / SMOE_G;
+    uint4 va[RB][CPL], vb[RB][CPL];
+    uint16_t sva[RB][CPL], svb[RB][CPL];
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+        const size_t row = row0 + i;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const uint32_t c = min(lane + WAVE * j, nch - 1);
+            va[i][j] = load_stream_u4(pa + row * row_bytes + c * 16);
+            vb[i][j] = load_stream_u4(pb + row * row_bytes + c * 16);
+            sva[i][j] = load_stream_u16(sa + row * row_scales + (c * 32) / SMOE_G);
+            svb[i][j] = load_stream_u16(sb + row * row_scales + (c * 32) / SMOE_G);
+        }
+    }
+    float* o = h + (static_cast<size_t>(tok) * d.K + r) * d.I;
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+        float ga = 0.f, ua = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            ga = fmaf(f16_bits_to_f32(sva[i][j]), q4_chunk_dot8(va[i][j], qa[j]), ga);
+            ua = fmaf(f16_bits_to_f32(svb[i][j]), q4_chunk_dot8(vb[i][j], qa[j]), ua);
+        }
+        ga = wave_sum(ga);
+        ua = wave_sum(ua);
+        // silu(z) = z * (1 / (1 + exp(-z)))  (kernels.metal:61-63, :334-336)
+        if (lane == 0) o[row0 + i] = (ga * (1.0f / (1.0f + expf(-ga)))) * ua;
+    }
+}
+
+template <int CPL, int VPL>
+__global__ __launch_bounds__(WAVE)
+void k_moe_up(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint64_t* __restrict__ ll_all,
+              float* __restrict__ h, uint32_t* __restrict__ ids_out, float* __restrict__ w_out,
+              ExpertPtrs* __restrict__ tbl_out, uint32_t* __restrict__ err)
+{
+    const uint32_t tok = blockIdx.z;
+    const float* hv = hidden + static_cast<size_t>(tok) * d.D;
+    uint64_t* ll = ll_all + static_cast<size_t>(tok) * (d.E + 1);
+    const uint32_t b = blockIdx.y * gridDim.x + blockIdx.x;
+    if (b < d.E)
+        moe_up_body<CPL, VPL, true>(d, L, hv, ll, h, ids_out, w_out, tbl_out, err, b);
+    else
+        moe_up_body<CPL, VPL, false>(d, L, hv, ll, h, ids_out, w_out, tbl_out, err, b);
 }
 
 // ---------------------------------------------------------------------------
@@ -292,27 +498,6 @@ void k_q4_rows(MoeDims d, const ExpertPtrs* __restrict__ tbl, uint32_t n_exp,
 
     float xr[CPL][32];
     float xsum[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const uint32_t c = lane + WAVE * j;
-        xsum[j] = 0.f;
-        if (c < nch) {
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const float4 v = load_f4(xv + c * 32 + q * 4);
-                xr[j][q * 4 + 0] = v.x;
-                xr[j][q * 4 + 1] = v.y;
-                xr[j][q * 4 + 2] = v.z;
-                xr[j][q * 4 + 3] = v.w;
-            }
-#pragma unroll
-            for (int q = 0; q < 32; ++q) xsum[j] += xr[j][q];
-        } else {
-#pragma unroll
-            for (int q = 0; q < 32; ++q) xr[j][q] = 0.f;
-        }
-    }
-
     uint4 va[RB][CPL], vb[RB][CPL];
     uint16_t sva[RB][CPL], svb[RB][CPL];
 #pragma unroll
@@ -320,16 +505,30 @@ void k_q4_rows(MoeDims d, const ExpertPtrs* __restrict__ tbl, uint32_t n_exp,
         const size_t row = row0 + i;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            const uint32_t c = lane + WAVE * j;
-            if (c < nch) {
-                va[i][j] = load_stream_u4(pa + row * row_bytes + c * 16);
-                sva[i][j] = load_stream_u16(sa + row * row_scales + (c * 32) / d.group);
-                if (GATE_UP) {
-                    vb[i][j] = load_stream_u4(pb + row * row_bytes + c * 16);
-                    svb[i][j] = load_stream_u16(sb + row * row_scales + (c * 32) / d.group);
-                }
+            const uint32_t c = min(lane + WAVE * j, nch - 1);
+            va[i][j] = load_stream_u4(pa + row * row_bytes + c * 16);
+            sva[i][j] = load_stream_u16(sa + row * row_scales + (c * 32) / d.group);
+            if (GATE_UP) {
+                vb[i][j] = load_stream_u4(pb + row * row_bytes + c * 16);
+                svb[i][j] = load_stream_u16(sb + row * row_scales + (c * 32) / d.group);
             }
         }
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const uint32_t c = min(lane + WAVE * j, nch - 1);
+        const bool ok = lane + WAVE * j < nch;
+        xsum[j] = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 v = load_f4(xv + c * 32 + q * 4);
+            xr[j][q * 4 + 0] = ok ? v.x : 0.f;
+            xr[j][q * 4 + 1] = ok ? v.y : 0.f;
+            xr[j][q * 4 + 2] = ok ? v.z : 0.f;
+            xr[j][q * 4 + 3] = ok ? v.w : 0.f;
+        }
+#pragma unroll
+        for (int q = 0; q < 32; ++q) xsum[j] += xr[j][q];
     }
     float* o = out + static_cast<size_t>(tok) * out_tok_stride + static_cast<size_t>(e.slot) * out_stride;
 #pragma unroll
@@ -337,12 +536,9 @@ void k_q4_rows(MoeDims d, const ExpertPtrs* __restrict__ tbl, uint32_t n_exp,
         float aa = 0.f, ab = 0.f;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            const uint32_t c = lane + WAVE * j;
-            if (c < nch) {
-                aa += q4_chunk_epilogue(f16_bits_to_f32(sva[i][j]), q4_chunk_dot(va[i][j], xr[j]), xsum[j]);
-                if (GATE_UP)
-                    ab += q4_chunk_epilogue(f16_bits_to_f32(svb[i][j]), q4_chunk_dot(vb[i][j], xr[j]), xsum[j]);
-            }
+            aa += q4_chunk_epilogue(f16_bits_to_f32(sva[i][j]), q4_chunk_dot(va[i][j], xr[j]), xsum[j]);
+            if (GATE_UP)
+                ab += q4_chunk_epilogue(f16_bits_to_f32(svb[i][j]), q4_chunk_dot(vb[i][j], xr[j]), xsum[j]);
         }
         aa = wave_sum(aa);
         if (GATE_UP) ab = wave_sum(ab);
@@ -354,16 +550,24 @@ void k_q4_rows(MoeDims d, const ExpertPtrs* __restrict__ tbl, uint32_t n_exp,
 }
 
 // ---------------------------------------------------------------------------
-// k_down_combine
+// k_down_combine: hidden[row] += sum_r w_r * (down_r[row] . h_r).
+// Lane p of the block owns (expert, 32-column chunk) pair p of the k experts'
+// down rows; its 32 h values are converted once to 4-bit digit words and reused
+// for the block's DOWN_RB rows.  Each row of all k experts is one reduction.
 // ---------------------------------------------------------------------------
-constexpr int DOWN_RB = 4;
+constexpr int DOWN_RB = 8;
 constexpr int DOWN_MAX_WAVES = 8;
 
 template <int PPL>
 __global__ __launch_bounds__(DOWN_MAX_WAVES * WAVE)
 void k_down_combine(MoeDims d, const ExpertPtrs* __restrict__ tbl, const float* __restrict__ h,
-                    const float* __restrict__ w, float* __restrict__ hidden)
+                    const float* __restrict__ w, float* __restrict__ hidden, uint64_t* __restrict__ ll_all)
 {
+    constexpr int G = 64;
+    // re-arm the routing exchange words of this token for the next k_moe_up
+    // (every k_moe_up that read them has finished: this is the next kernel)
+    if (blockIdx.x == 0)
+        for (uint32_t i = threadIdx.x; i <= d.E; i += blockDim.x) ll_all[static_cast<size_t>(blockIdx.y) * (d.E + 1) + i] = 0;
     __shared__ float part[DOWN_MAX_WAVES][DOWN_RB];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int nw = blockDim.x >> 6;
@@ -375,37 +579,23 @@ void k_down_combine(MoeDims d, const ExpertPtrs* __restrict__ tbl, const float* 
     hidden += static_cast<size_t>(tok) * d.D;
     const uint32_t cpr = d.I >> 5;
     const uint32_t npairs = d.K * cpr;
-    const uint32_t row_bytes = d.I >> 1, row_scales = d.I / d.group;
+    const uint32_t row_bytes = d.I >> 1, row_scales = d.I / G;
 
-    float hr[PPL][32];
-    float hsum[PPL], wr[PPL];
     const uint8_t* pd[PPL];
     const uint16_t* sd[PPL];
-    uint32_t cc[PPL];
+    uint32_t cc[PPL], rr[PPL];
     bool ok[PPL];
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
-        const uint32_t p = (wv * PPL + j) * WAVE + lane;
-        ok[j] = p < npairs;
-        const uint32_t rr = ok[j] ? p / cpr : 0;
-        cc[j] = ok[j] ? p - rr * cpr : 0;
-        pd[j] = tbl[rr].pd;
-        sd[j] = tbl[rr].sd;
-        wr[j] = w[rr];
-        hsum[j] = 0.f;
-        const float* hv = h + static_cast<size_t>(rr) * d.I + cc[j] * 32;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const float4 v = ok[j] ? load_f4(hv + q * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-            hr[j][q * 4 + 0] = v.x;
-            hr[j][q * 4 + 1] = v.y;
-            hr[j][q * 4 + 2] = v.z;
-            hr[j][q * 4 + 3] = v.w;
-        }
-#pragma unroll
-        for (int q = 0; q < 32; ++q) hsum[j] += hr[j][q];
+        const uint32_t p0 = (wv * PPL + j) * WAVE + lane;
+        ok[j] = p0 < npairs;
+        const uint32_t p = min(p0, npairs - 1);
+        rr[j] = p / cpr;
+        cc[j] = p - rr[j] * cpr;
+        pd[j] = tbl[rr[j]].pd;
+        sd[j] = tbl[rr[j]].sd;
     }
-
+    // weights first (HBM), then h (L2): both in flight together
     uint4 v[DOWN_RB][PPL];
     uint16_t sv[DOWN_RB][PPL];
 #pragma unroll
@@ -413,21 +603,34 @@ void k_down_combine(MoeDims d, const ExpertPtrs* __restrict__ tbl, const float* 
         const size_t row = row0 + i;
 #pragma unroll
         for (int j = 0; j < PPL; ++j) {
-            if (ok[j]) {
-                v[i][j] = load_stream_u4(pd[j] + row * row_bytes + cc[j] * 16);
-                sv[i][j] = load_stream_u16(sd[j] + row * row_scales + (cc[j] * 32) / d.group);
-            }
+            v[i][j] = load_stream_u4(pd[j] + row * row_bytes + cc[j] * 16);
+            sv[i][j] = load_stream_u16(sd[j] + row * row_scales + (cc[j] * 32) / G);
         }
+    }
+    Q4Act qh[PPL];
+    float wr[PPL];
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) {
+        wr[j] = ok[j] ? w[rr[j]] : 0.f;       // pairs past the end contribute nothing
+        const float* hv = h + static_cast<size_t>(rr[j]) * d.I + cc[j] * 32;
+        float a[32];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 t = load_f4(hv + q * 4);
+            a[q * 4 + 0] = t.x;
+            a[q * 4 + 1] = t.y;
+            a[q * 4 + 2] = t.z;
+            a[q * 4 + 3] = t.w;
+        }
+        q4_act_from_floats(a, qh[j]);
     }
 #pragma unroll
     for (int i = 0; i < DOWN_RB; ++i) {
         float acc = 0.f;
 #pragma unroll
         for (int j = 0; j < PPL; ++j) {
-            if (ok[j]) {
-                const float y = q4_chunk_epilogue(f16_bits_to_f32(sv[i][j]), q4_chunk_dot(v[i][j], hr[j]), hsum[j]);
-                acc = fmaf(wr[j], y, acc);
-            }
+            const float y = f16_bits_to_f32(sv[i][j]) * q4_chunk_dot8(v[i][j], qh[j]);
+            acc = fmaf(wr[j], y, acc);
         }
         acc = wave_sum(acc);
         if (lane == 0) part[wv][i] = acc;
@@ -444,31 +647,37 @@ void k_down_combine(MoeDims d, const ExpertPtrs* __restrict__ tbl, const float* 
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden,
-                        uint32_t n_tok, float* normed, float* logits, uint32_t* ids, float* w,
-                        ExpertPtrs* tbl, uint32_t* counter, hipStream_t s)
+template <int CPL>
+static void moe_up_c(dim3 grid, hipStream_t s, const MoeDims& d, const LayerDesc& L, const float* hidden,
+                     uint64_t* ll, float* h, uint32_t* ids, float* w, ExpertPtrs* tbl, uint32_t* err)
 {
-    const uint32_t nblk = (d.E + ROUTE_WAVES - 1) / ROUTE_WAVES;
-    const dim3 grid(nblk, n_tok), block(ROUTE_WAVES * WAVE);
-    const size_t lds = d.D * sizeof(float);
-    switch (topk_vpl(d.E)) {
-        case 1: hipLaunchKernelGGL(k_route<1>, grid, block, lds, s, d, L, hidden, normed, logits, ids, w, tbl, counter); break;
-        case 2: hipLaunchKernelGGL(k_route<2>, grid, block, lds, s, d, L, hidden, normed, logits, ids, w, tbl, counter); break;
-        case 4: hipLaunchKernelGGL(k_route<4>, grid, block, lds, s, d, L, hidden, normed, logits, ids, w, tbl, counter); break;
-        default: hipLaunchKernelGGL(k_route<8>, grid, block, lds, s, d, L, hidden, normed, logits, ids, w, tbl, counter); break;
-    }
+    if (d.E <= 128)
+        hipLaunchKernelGGL((k_moe_up<CPL, 2>), grid, dim3(WAVE), 0, s, d, L, hidden, ll, h, ids, w, tbl, err);
+    else
+        hipLaunchKernelGGL((k_moe_up<CPL, 8>), grid, dim3(WAVE), 0, s, d, L, hidden, ll, h, ids, w, tbl, err);
+}
+
+hipError_t launch_moe_up(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t n_tok, uint64_t* ll,
+                         float* h, uint32_t* ids, float* w, ExpertPtrs* tbl, uint32_t* err, hipStream_t s)
+{
+    if (d.group != 64 || d.E > SMOE_TOPK_MAX_N || d.I % UP_RB) return hipErrorInvalidValue;
+    const uint32_t row_blocks = d.I / UP_RB;                              // one wave per 8 rows
+    const dim3 grid(row_blocks, d.K, n_tok);
+    const uint32_t cpl = (d.D / 32 + WAVE - 1) / WAVE;   // 32-column chunks per lane
+    if (cpl == 1) moe_up_c<1>(grid, s, d, L, hidden, ll, h, ids, w, tbl, err);
+    else if (cpl == 2) moe_up_c<2>(grid, s, d, L, hidden, ll, h, ids, w, tbl, err);
+    else if (cpl <= 4) moe_up_c<4>(grid, s, d, L, hidden, ll, h, ids, w, tbl, err);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
 hipError_t launch_topk(const float* scores, uint32_t rows, uint32_t n, uint32_t k,
                        uint32_t norm, uint32_t* ids, float* w, hipStream_t s)
 {
-    switch (topk_vpl(n)) {
-        case 1: hipLaunchKernelGGL(k_topk<1>, dim3(rows), dim3(WAVE), 0, s, scores, n, k, norm, ids, w); break;
-        case 2: hipLaunchKernelGGL(k_topk<2>, dim3(rows), dim3(WAVE), 0, s, scores, n, k, norm, ids, w); break;
-        case 4: hipLaunchKernelGGL(k_topk<4>, dim3(rows), dim3(WAVE), 0, s, scores, n, k, norm, ids, w); break;
-        default: hipLaunchKernelGGL(k_topk<8>, dim3(rows), dim3(WAVE), 0, s, scores, n, k, norm, ids, w); break;
-    }
+    if (topk_vpl(n) == 2)
+        hipLaunchKernelGGL(k_topk<2>, dim3(rows), dim3(WAVE), 0, s, scores, n, k, norm, ids, w);
+    else
+        hipLaunchKernelGGL(k_topk<8>, dim3(rows), dim3(WAVE), 0, s, scores, n, k, norm, ids, w);
     return hipGetLastError();
 }
 
@@ -520,8 +729,8 @@ hipError_t launch_down_slots(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n
                               tbl_tok_stride, out_tok_stride, s);
 }
 
-hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const float* h,
-                               const float* w, float* hidden, uint32_t n_tok, hipStream_t s)
+hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const float* h, const float* w,
+                               float* hidden, uint64_t* ll, uint32_t n_tok, hipStream_t s)
 {
     const uint32_t npairs = d.K * (d.I / 32);
     int ppl = npairs <= 64 ? 1 : npairs <= 128 ? 2 : 3;
@@ -533,10 +742,10 @@ hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const fl
     }
     dim3 grid(d.D / DOWN_RB, n_tok), block(nw * WAVE);
     switch (ppl) {
-        case 1: hipLaunchKernelGGL(k_down_combine<1>, grid, block, 0, s, d, tbl, h, w, hidden); break;
-        case 2: hipLaunchKernelGGL(k_down_combine<2>, grid, block, 0, s, d, tbl, h, w, hidden); break;
-        case 3: hipLaunchKernelGGL(k_down_combine<3>, grid, block, 0, s, d, tbl, h, w, hidden); break;
-        default: hipLaunchKernelGGL(k_down_combine<4>, grid, block, 0, s, d, tbl, h, w, hidden); break;
+        case 1: hipLaunchKernelGGL(k_down_combine<1>, grid, block, 0, s, d, tbl, h, w, hidden, ll); break;
+        case 2: hipLaunchKernelGGL(k_down_combine<2>, grid, block, 0, s, d, tbl, h, w, hidden, ll); break;
+        case 3: hipLaunchKernelGGL(k_down_combine<3>, grid, block, 0, s, d, tbl, h, w, hidden, ll); break;
+        default: hipLaunchKernelGGL(k_down_combine<4>, grid, block, 0, s, d, tbl, h, w, hidden, ll); break;
     }
     return hipGetLastError();
 }

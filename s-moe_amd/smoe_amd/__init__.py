@@ -90,9 +90,9 @@ SIGNATURES = [
     ("smoe_hip_last_error", C.c_char_p, [_VP]),
 ]
 
-KERNEL_ROUTE, KERNEL_GATE_UP, KERNEL_DOWN_COMBINE, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
+KERNEL_MOE_UP, KERNEL_GATE_UP, KERNEL_MOE_DOWN, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
 KERNEL_PERMUTE, KERNEL_GROUPED_GATE_UP, KERNEL_GROUPED_DOWN, KERNEL_SCATTER = 5, 6, 7, 8
-KERNEL_NAMES = {0: "route", 1: "gate_up", 2: "down_combine", 3: "down_slots", 4: "topk",
+KERNEL_NAMES = {0: "moe_up", 1: "gate_up", 2: "moe_down", 3: "down_slots", 4: "topk",
                 5: "permute", 6: "grouped_gate_up", 7: "grouped_down", 8: "scatter"}
 
 _lib = None
