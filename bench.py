@@ -131,6 +131,10 @@ def main():
     ms_per_step = elapsed * 1e3 / args.steps
     tok_s = args.steps / elapsed
 
+    if args.profile_steps <= 0:
+        print(json.dumps({"value": round(tok_s, 2), "ms_per_step": round(ms_per_step, 4)}), flush=True)
+        ctx.close()
+        return
     # per-kernel durations: HIP events around each launch on the launch stream
     ctx.profile_enable(True)
     for _ in range(args.profile_steps):

@@ -29,7 +29,7 @@ constexpr uint32_t kEvents = 256;              // handle ring
 struct DeviceScratch {
     // capacities
     uint32_t D = 0, E = 0, K = 0, I = 0, T = 0;
-    uint64_t* ll = nullptr;      // [T x (E+1)] routing exchange words
+    uint64_t* ll = nullptr;      // [T x ll_token_words(E)] routing exchange words
     uint32_t* err = nullptr;     // [1] device-side error flags
     uint32_t* ids = nullptr;     // [T x K]
     float* w = nullptr;          // [T x K]
@@ -186,10 +186,10 @@ int ensure_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
     n.T = std::max(c.T, T);
     free_device_scratch(c);
     const size_t T_ = n.T;
-    bool ok = dalloc(ctx, &n.ll, T_ * (n.E + 1)) && dalloc(ctx, &n.err, 1) && dalloc(ctx, &n.ids, T_ * n.K) &&
+    bool ok = dalloc(ctx, &n.ll, T_ * smoe::ll_token_words(n.E)) && dalloc(ctx, &n.err, 1) && dalloc(ctx, &n.ids, T_ * n.K) &&
               dalloc(ctx, &n.w, T_ * n.K) && dalloc(ctx, &n.tbl, T_ * n.K) && dalloc(ctx, &n.h, T_ * n.K * n.I);
     // the exchange words start disarmed; every launch pair leaves them so
-    ok = ok && hip_ok(ctx, hipMemset(n.ll, 0, T_ * (n.E + 1) * sizeof(uint64_t)), "hipMemset") &&
+    ok = ok && hip_ok(ctx, hipMemset(n.ll, 0, T_ * smoe::ll_token_words(n.E) * sizeof(uint64_t)), "hipMemset") &&
          hip_ok(ctx, hipMemset(n.err, 0, sizeof(uint32_t)), "hipMemset");
     if (!ok) {
         free_device_scratch(n);

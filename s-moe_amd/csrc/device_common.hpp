@@ -12,6 +12,8 @@ namespace smoe {
 
 constexpr int WAVE = 64;
 
+constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
+
 // ---- number formats ------------------------------------------------------
 __device__ __forceinline__ float bf16_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
 
@@ -112,6 +114,78 @@ __device__ __forceinline__ float wave_max(float v)
     v = fmaxf(v, dpp_f32<DPP_ROW_BCAST15, 0xA>(-INFINITY, v));
     v = fmaxf(v, dpp_f32<DPP_ROW_BCAST31, 0xC>(-INFINITY, v));
     return readlane_f32(v, 63);
+}
+
+// ---- transposed reduction of N per-lane values ---------------------------
+// Sums value i (i < N, N a power of two <= 16) over the 64 lanes for all i at
+// once: each butterfly step over a lane bit halves the values a lane holds
+// (lanes with the bit clear keep the lower half of the indices, the others the
+// upper half), so N sums cost about N + 6 cross-lane ops instead of 7 N.
+// Lane l returns the total of value l >> (6 - log2 N).
+//   bit 5: v_permlane32_swap (lanes 32-63 of the first operand <-> lanes 0-31
+//          of the second), bit 4: v_permlane16_swap (odd rows of the first
+//          operand <-> even rows of the second), bit 3: row_ror:8 (lane ^ 8),
+//   bit 2: row_half_mirror (lane -> 7 - lane within 8: flips bit 2; the lower
+//          bits are summed over afterwards), bits 1, 0: quad_perm.
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+
+__device__ __forceinline__ void swap32_sum(float& lo, float hi)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    lo = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void swap16_sum(float& lo, float hi)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    lo = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+template <int CTRL>
+__device__ __forceinline__ void dpp_split_sum(float& lo, float hi, bool upper)
+{
+    const float keep = upper ? hi : lo;
+    const float send = upper ? lo : hi;
+    lo = keep + dpp_f32<CTRL>(0.f, send);
+}
+
+template <int N>
+__device__ __forceinline__ float wave_sum_rows(const float (&v)[N])
+{
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "N must be a power of two <= 16");
+    const int lane = threadIdx.x & 63;
+    float a[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) a[i] = v[i];
+    // bit 5
+    if constexpr (N >= 2) {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) swap32_sum(a[i], a[i + N / 2]);
+    } else {
+        swap32_sum(a[0], a[0]);
+    }
+    // bit 4
+    if constexpr (N >= 4) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) swap16_sum(a[i], a[i + N / 4]);
+    } else {
+        swap16_sum(a[0], a[0]);
+    }
+    // bit 3
+    if constexpr (N >= 8) {
+#pragma unroll
+        for (int i = 0; i < N / 8; ++i) dpp_split_sum<DPP_ROW_ROR8>(a[i], a[i + N / 8], lane & 8);
+    } else {
+        a[0] += dpp_f32<DPP_ROW_ROR8>(0.f, a[0]);
+    }
+    // bit 2
+    if constexpr (N >= 16) {
+        dpp_split_sum<DPP_ROW_HALF_MIRROR>(a[0], a[1], lane & 4);
+    } else {
+        a[0] += dpp_f32<DPP_ROW_HALF_MIRROR>(0.f, a[0]);
+    }
+    // bits 1, 0
+    a[0] += dpp_f32<DPP_QUAD_XOR2>(0.f, a[0]);
+    a[0] += dpp_f32<DPP_QUAD_XOR1>(0.f, a[0]);
+    return a[0];
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)

@@ -11,6 +11,13 @@ namespace smoe {
 constexpr int SMOE_TOPK_MAX_N = 512;
 constexpr int SMOE_TOPK_MAX_K = 16;
 
+// Routing exchange of one token: LL_COPIES copies of its E logit words (flag
+// in the high half), ll_copy_words(E) words apart (> 4 KB), so the waves that
+// poll them spread over several memory channels instead of queueing on one.
+constexpr uint32_t LL_COPIES = 8;
+__host__ __device__ constexpr uint32_t ll_copy_words(uint32_t E) { return (E > 512u ? E : 512u) + 32u; }
+__host__ __device__ constexpr size_t ll_token_words(uint32_t E) { return size_t(LL_COPIES) * ll_copy_words(E); }
+
 // Six tensor pointers of one expert plus the scratch slot its results use.
 struct ExpertPtrs {
     const uint8_t*  pg;

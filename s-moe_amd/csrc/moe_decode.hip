@@ -117,20 +117,20 @@ __device__ void topk_select(float (&p)[VPL], uint32_t (&id)[VPL], uint32_t (&key
 
 // ---------------------------------------------------------------------------
 // Softmax + top-k of n scores held in one wave (position p = lane + 64 j).
-// Fast path: a radix select over the probability bits finds the m-th largest
-// key (m = count + 1 when count < n), the m candidates are ranked among
-// themselves; when those m probabilities are pairwise distinct (and no
-// probability is NaN) the reference's k rounds of selection with swaps
-// (scout.cpp:101-110) pick exactly ranks 0..count-1.  Any tie falls back to
-// the exact swap emulation topk_select.  Lane r < count receives (id_r, w_r).
+// Fast path: count rounds of max extraction.  Round s takes the wave maximum
+// of the remaining keys; when exactly one position holds it, that position is
+// what the reference's round s of selection with swaps (scout.cpp:101-110)
+// picks, whatever the earlier swaps moved, since a strict maximum wins the
+// strict '>' scan from any arrangement.  A maximum held by two positions (a
+// tie, where positions and swaps decide) or any NaN sends the row to the
+// exact swap emulation topk_select.  A unique maximum in the last round also
+// proves it strictly above every unselected key.
+// Lane r < count receives (id_r, w_r); returns count.
 // ---------------------------------------------------------------------------
 template <int VPL>
 __device__ uint32_t topk_fast(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t norm, uint32_t& my_id,
                               float& my_w)
 {
-    __shared__ uint32_t c_key[SMOE_TOPK_MAX_K + 1];
-    __shared__ uint32_t c_pos[SMOE_TOPK_MAX_K + 1];
-    __shared__ float c_p[SMOE_TOPK_MAX_K + 1];
     const int lane = threadIdx.x & (WAVE - 1);
     // softmax (scout.cpp:85-98)
     float m = -INFINITY;
@@ -158,62 +158,42 @@ __device__ uint32_t topk_fast(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t 
         key[j] = pos < n ? (isnan(v[j]) ? 1u : __float_as_uint(v[j]) + 1u) : 0u;
     }
     const uint32_t count = k < n ? k : n;
-    const uint32_t msel = count < n ? count + 1 : count;
-    bool fast = __ballot(nan) == 0;
-    if (fast) {
-        // m-th largest key: keys are at most bits(1.0f) + 1 < 2^30
-        uint32_t T = 0;
-        for (int bit = 29; bit >= 0; --bit) {
-            const uint32_t cand = T | (1u << bit);
-            uint32_t c = 0;
+    if (__ballot(nan) == 0) {
+        uint32_t rem[VPL];
 #pragma unroll
-            for (int j = 0; j < VPL; ++j) c += __popcll(__ballot(key[j] >= cand));
-            if (c >= msel) T = cand;
-        }
-        uint32_t base = 0;
+        for (int j = 0; j < VPL; ++j) rem[j] = key[j];
+        uint32_t rid = 0;
+        float rw = 0.f, ksum = 0.f;
+        bool unique = true;
+        for (uint32_t s = 0; s < count && unique; ++s) {
+            uint32_t lk = rem[0];
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) {
-            const uint64_t mk = __ballot(key[j] >= T);
-            if (key[j] >= T) {
-                const uint32_t slot = base + __popcll(mk & ((1ull << lane) - 1ull));
-                if (slot <= SMOE_TOPK_MAX_K) {
-                    c_key[slot] = key[j];
-                    c_pos[slot] = id[j];
-                    c_p[slot] = v[j];
-                }
+            for (int j = 1; j < VPL; ++j) lk = max(lk, rem[j]);
+            const uint32_t kmax = wave_max_u32(lk);
+            uint32_t hits = 0, pos = 0;
+#pragma unroll
+            for (int j = VPL - 1; j >= 0; --j) {
+                const uint64_t b = __ballot(rem[j] == kmax);
+                hits += __popcll(b);
+                if (b != 0) pos = WAVE * j + __builtin_ctzll(b);
+                if (rem[j] == kmax) rem[j] = 0u;
             }
-            base += __popcll(mk);
+            unique = hits == 1;
+            const float ps = readlane_f32(sel(v, pos >> 6), pos & 63);
+            ksum += ps;                                 // rank order, as the reference
+            if (static_cast<uint32_t>(lane) == s) {
+                rid = pos;
+                rw = ps;
+            }
         }
-        fast = base == msel;          // no tie across the boundary
-        if (fast) {
-            __builtin_amdgcn_wave_barrier();
-            uint32_t rank = 0;
-            bool dup = false;
-            const uint32_t kr = static_cast<uint32_t>(lane) < msel ? c_key[lane] : 0u;
-            for (uint32_t q = 0; q < msel; ++q) {
-                const uint32_t kq = c_key[q];
-                rank += kq > kr;
-                dup |= (kq == kr) && (q != static_cast<uint32_t>(lane));
-            }
-            fast = __ballot(static_cast<uint32_t>(lane) < msel && dup) == 0;
-            const uint32_t pr = static_cast<uint32_t>(lane) < msel ? c_pos[lane] : 0u;
-            const float wr = static_cast<uint32_t>(lane) < msel ? c_p[lane] : 0.f;
-            __builtin_amdgcn_wave_barrier();
-            if (fast && static_cast<uint32_t>(lane) < msel) {
-                c_pos[rank] = pr;
-                c_p[rank] = wr;
-            }
-            __builtin_amdgcn_wave_barrier();
-            if (fast) {
-                float ksum = 0.f;
-                for (uint32_t r = 0; r < count; ++r) ksum += c_p[r];   // sequential, as the reference
-                my_id = static_cast<uint32_t>(lane) < count ? c_pos[lane] : 0u;
-                my_w = static_cast<uint32_t>(lane) < count ? c_p[lane] : 0.f;
-                if (norm && ksum > 0.f) my_w = my_w * (1.0f / ksum);
-            }
+        if (unique) {
+            my_id = rid;
+            my_w = rw;
+            if (norm && ksum > 0.f) my_w = my_w * (1.0f / ksum);
+            return count;
         }
     }
-    if (!fast) topk_select<VPL>(v, id, key, count, norm, my_id, my_w);
+    topk_select<VPL>(v, id, key, count, norm, my_id, my_w);
     return count;
 }
 
@@ -349,7 +329,9 @@ __device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L
                 }
             }
             acc = wave_sum(acc);
-            if (lane == 0) __hip_atomic_store(ll + row, ll_word(acc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane < static_cast<int>(LL_COPIES))
+                __hip_atomic_store(ll + lane * ll_copy_words(d.E) + row, ll_word(acc), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             row += nb;
             if (row >= d.E) break;
             const uint16_t* wr = L.router_w + static_cast<size_t>(row) * D;
@@ -361,21 +343,22 @@ __device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L
             }
         }
     }
-    // 5. wait for the E logits, then select
+    // 5. wait for the E logits (in this block's copy), then select
     float v[VPL];
     {
+        const uint64_t* llc = ll + (b % LL_COPIES) * ll_copy_words(d.E);
         uint32_t spins = 0;
         bool all;
         do {
             all = true;
+            // every load issued before any is waited on (padding lanes re-read word E-1)
 #pragma unroll
             for (int j = 0; j < VPL; ++j) {
                 const uint32_t pos = lane + WAVE * j;
-                if (pos < d.E) {
-                    const uint64_t w64 = __hip_atomic_load(ll + pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    v[j] = __uint_as_float(static_cast<uint32_t>(w64));
-                    all &= (w64 >> 32) != 0;
-                }
+                const uint64_t w64 =
+                    __hip_atomic_load(llc + min(pos, d.E - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                v[j] = __uint_as_float(static_cast<uint32_t>(w64));
+                all &= pos >= d.E || (w64 >> 32) != 0;
             }
             all = __ballot(!all) == 0;
             if (!all && ++spins > SPIN_LIMIT) {
@@ -428,7 +411,9 @@ __device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L
             svb[i][j] = load_stream_u16(sb + row * row_scales + (c * 32) / SMOE_G);
         }
     }
-    float* o = h + (static_cast<size_t>(tok) * d.K + r) * d.I;
+    __builtin_amdgcn_sched_barrier(0);
+    // per-lane partial dots: value 2i = gate row i, 2i + 1 = up row i
+    float part[2 * RB];
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
         float ga = 0.f, ua = 0.f;
@@ -437,11 +422,17 @@ __device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L
             ga = fmaf(f16_bits_to_f32(sva[i][j]), q4_chunk_dot8(va[i][j], qa[j]), ga);
             ua = fmaf(f16_bits_to_f32(svb[i][j]), q4_chunk_dot8(vb[i][j], qa[j]), ua);
         }
-        ga = wave_sum(ga);
-        ua = wave_sum(ua);
-        // silu(z) = z * (1 / (1 + exp(-z)))  (kernels.metal:61-63, :334-336)
-        if (lane == 0) o[row0 + i] = (ga * (1.0f / (1.0f + expf(-ga)))) * ua;
+        part[2 * i] = ga;
+        part[2 * i + 1] = ua;
     }
+    // lane l holds the total of value l >> SH
+    constexpr int SH = 6 - ilog2(2 * RB);
+    const float tot = wave_sum_rows<2 * RB>(part);
+    const float gv = __shfl(tot, (2 * lane) << SH);
+    const float uv = __shfl(tot, (2 * lane + 1) << SH);
+    // silu(z) = z * (1 / (1 + exp(-z)))  (kernels.metal:61-63, :334-336), all rows at once
+    float* o = h + (static_cast<size_t>(tok) * d.K + r) * d.I;
+    if (lane < RB) o[row0 + lane] = (gv * (1.0f / (1.0f + expf(-gv)))) * uv;
 }
 
 template <int CPL, int VPL>
@@ -452,7 +443,7 @@ void k_moe_up(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint64_t
 {
     const uint32_t tok = blockIdx.z;
     const float* hv = hidden + static_cast<size_t>(tok) * d.D;
-    uint64_t* ll = ll_all + static_cast<size_t>(tok) * (d.E + 1);
+    uint64_t* ll = ll_all + static_cast<size_t>(tok) * ll_token_words(d.E);
     const uint32_t b = blockIdx.y * gridDim.x + blockIdx.x;
     if (b < d.E)
         moe_up_body<CPL, VPL, true>(d, L, hv, ll, h, ids_out, w_out, tbl_out, err, b);
@@ -552,8 +543,12 @@ void k_q4_rows(MoeDims d, const ExpertPtrs* __restrict__ tbl, uint32_t n_exp,
 // ---------------------------------------------------------------------------
 // k_down_combine: hidden[row] += sum_r w_r * (down_r[row] . h_r).
 // Lane p of the block owns (expert, 32-column chunk) pair p of the k experts'
-// down rows; its 32 h values are converted once to 4-bit digit words and reused
-// for the block's DOWN_RB rows.  Each row of all k experts is one reduction.
+// down rows (PPL pairs per lane); its 32 h values are turned into digit words
+// once and reused for the block's DOWN_RB rows, so each row of all k experts
+// is one block-wide reduction: a transposed wave reduction over the rows,
+// then the waves' partials through LDS.  Loads go out in dependency order:
+// expert table and h first, the down weights as soon as the table lands; the
+// h conversion overlaps the weight fetch.
 // ---------------------------------------------------------------------------
 constexpr int DOWN_RB = 8;
 constexpr int DOWN_MAX_WAVES = 8;
@@ -563,15 +558,18 @@ __global__ __launch_bounds__(DOWN_MAX_WAVES * WAVE)
 void k_down_combine(MoeDims d, const ExpertPtrs* __restrict__ tbl, const float* __restrict__ h,
                     const float* __restrict__ w, float* __restrict__ hidden, uint64_t* __restrict__ ll_all)
 {
-    constexpr int G = 64;
+    constexpr int RB = DOWN_RB;
     // re-arm the routing exchange words of this token for the next k_moe_up
     // (every k_moe_up that read them has finished: this is the next kernel)
-    if (blockIdx.x == 0)
-        for (uint32_t i = threadIdx.x; i <= d.E; i += blockDim.x) ll_all[static_cast<size_t>(blockIdx.y) * (d.E + 1) + i] = 0;
-    __shared__ float part[DOWN_MAX_WAVES][DOWN_RB];
+    if (blockIdx.x == 0) {
+        uint64_t* ll = ll_all + static_cast<size_t>(blockIdx.y) * ll_token_words(d.E);
+        for (uint32_t i = threadIdx.x; i < LL_COPIES * d.E; i += blockDim.x)
+            ll[(i / d.E) * ll_copy_words(d.E) + i % d.E] = 0;
+    }
+    __shared__ float part[DOWN_MAX_WAVES][RB];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int nw = blockDim.x >> 6;
-    const uint32_t row0 = blockIdx.x * DOWN_RB;
+    const uint32_t row0 = blockIdx.x * RB;
     const uint32_t tok = blockIdx.y;
     tbl += static_cast<size_t>(tok) * d.K;
     h += static_cast<size_t>(tok) * d.K * d.I;
@@ -579,12 +577,14 @@ void k_down_combine(MoeDims d, const ExpertPtrs* __restrict__ tbl, const float* 
     hidden += static_cast<size_t>(tok) * d.D;
     const uint32_t cpr = d.I >> 5;
     const uint32_t npairs = d.K * cpr;
-    const uint32_t row_bytes = d.I >> 1, row_scales = d.I / G;
+    const uint32_t row_bytes = d.I >> 1, row_scales = d.I / SMOE_G;
 
     const uint8_t* pd[PPL];
     const uint16_t* sd[PPL];
     uint32_t cc[PPL], rr[PPL];
     bool ok[PPL];
+    float4 hx[PPL][8];
+    float wr[PPL];
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
         const uint32_t p0 = (wv * PPL + j) * WAVE + lane;
@@ -595,48 +595,56 @@ void k_down_combine(MoeDims d, const ExpertPtrs* __restrict__ tbl, const float* 
         pd[j] = tbl[rr[j]].pd;
         sd[j] = tbl[rr[j]].sd;
     }
-    // weights first (HBM), then h (L2): both in flight together
-    uint4 v[DOWN_RB][PPL];
-    uint16_t sv[DOWN_RB][PPL];
 #pragma unroll
-    for (int i = 0; i < DOWN_RB; ++i) {
+    for (int j = 0; j < PPL; ++j) {
+        const float* hv = h + static_cast<size_t>(rr[j]) * d.I + cc[j] * 32;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) hx[j][q] = load_f4(hv + q * 4);
+        wr[j] = w[rr[j]];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 v[RB][PPL];
+    uint16_t sv[RB][PPL];
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
         const size_t row = row0 + i;
 #pragma unroll
         for (int j = 0; j < PPL; ++j) {
             v[i][j] = load_stream_u4(pd[j] + row * row_bytes + cc[j] * 16);
-            sv[i][j] = load_stream_u16(sd[j] + row * row_scales + (cc[j] * 32) / G);
+            sv[i][j] = load_stream_u16(sd[j] + row * row_scales + (cc[j] * 32) / SMOE_G);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
     Q4Act qh[PPL];
-    float wr[PPL];
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
-        wr[j] = ok[j] ? w[rr[j]] : 0.f;       // pairs past the end contribute nothing
-        const float* hv = h + static_cast<size_t>(rr[j]) * d.I + cc[j] * 32;
         float a[32];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const float4 t = load_f4(hv + q * 4);
-            a[q * 4 + 0] = t.x;
-            a[q * 4 + 1] = t.y;
-            a[q * 4 + 2] = t.z;
-            a[q * 4 + 3] = t.w;
+            a[q * 4 + 0] = hx[j][q].x;
+            a[q * 4 + 1] = hx[j][q].y;
+            a[q * 4 + 2] = hx[j][q].z;
+            a[q * 4 + 3] = hx[j][q].w;
         }
         q4_act_from_floats(a, qh[j]);
+        if (!ok[j]) wr[j] = 0.f;   // pairs past the end contribute nothing
     }
+    float acc[RB];
 #pragma unroll
-    for (int i = 0; i < DOWN_RB; ++i) {
-        float acc = 0.f;
+    for (int i = 0; i < RB; ++i) {
+        acc[i] = 0.f;
 #pragma unroll
         for (int j = 0; j < PPL; ++j) {
             const float y = f16_bits_to_f32(sv[i][j]) * q4_chunk_dot8(v[i][j], qh[j]);
-            acc = fmaf(wr[j], y, acc);
+            acc[i] = fmaf(wr[j], y, acc[i]);
         }
-        acc = wave_sum(acc);
-        if (lane == 0) part[wv][i] = acc;
     }
+    // lane l holds the wave's total of row l >> SH
+    constexpr int SH = 6 - ilog2(RB);
+    const float tot = wave_sum_rows<RB>(acc);
+    if ((lane & ((1 << SH) - 1)) == 0) part[wv][lane >> SH] = tot;
     __syncthreads();
-    if (threadIdx.x < DOWN_RB) {
+    if (threadIdx.x < RB) {
         float t = 0.f;
         for (int q = 0; q < nw; ++q) t += part[q][threadIdx.x];
         const uint32_t row = row0 + threadIdx.x;
@@ -732,19 +740,16 @@ hipError_t launch_down_slots(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n
 hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const float* h, const float* w,
                                float* hidden, uint64_t* ll, uint32_t n_tok, hipStream_t s)
 {
+    // one (expert, chunk) pair per lane while the block fits in DOWN_MAX_WAVES waves
     const uint32_t npairs = d.K * (d.I / 32);
-    int ppl = npairs <= 64 ? 1 : npairs <= 128 ? 2 : 3;
-    uint32_t nw = (npairs + 64u * ppl - 1) / (64u * ppl);
-    if (nw > DOWN_MAX_WAVES) {
-        ppl = 4;
-        nw = (npairs + 255u) / 256u;
-        if (nw > DOWN_MAX_WAVES) return hipErrorInvalidValue;
-    }
+    uint32_t ppl = 1;
+    while (ppl < 4 && (npairs + 64u * ppl - 1) / (64u * ppl) > DOWN_MAX_WAVES) ppl *= 2;
+    const uint32_t nw = (npairs + 64u * ppl - 1) / (64u * ppl);
+    if (nw > DOWN_MAX_WAVES || d.D % DOWN_RB) return hipErrorInvalidValue;
     dim3 grid(d.D / DOWN_RB, n_tok), block(nw * WAVE);
     switch (ppl) {
         case 1: hipLaunchKernelGGL(k_down_combine<1>, grid, block, 0, s, d, tbl, h, w, hidden, ll); break;
         case 2: hipLaunchKernelGGL(k_down_combine<2>, grid, block, 0, s, d, tbl, h, w, hidden, ll); break;
-        case 3: hipLaunchKernelGGL(k_down_combine<3>, grid, block, 0, s, d, tbl, h, w, hidden, ll); break;
         default: hipLaunchKernelGGL(k_down_combine<4>, grid, block, 0, s, d, tbl, h, w, hidden, ll); break;
     }
     return hipGetLastError();
