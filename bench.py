@@ -10,14 +10,18 @@ blocks (RMSNorm -> router -> top-k -> fused Q4 expert FFN -> weighted combine
 once as a HIP graph and replayed.
 
     python bench.py [--gpus 1] [--steps 256] [--warmup 16] [--config 30b|235b]
+    python bench.py --rocprof-summary DIR [--pmc-out FILE]   (summarise a rocprofv3 run)
 
-Prints one JSON line (metric, value = tok/s, roofline of the dominant kernel
-from HIP events on its own stream, cpu_baseline = the oracle timed on a
-bounded sample on this host).
+Prints one JSON line: metric, value = tok/s over the timed replays, the
+roofline of the dominant kernel (its average duration from HIP start/stop
+events that its own dispatches record on the launch stream), and
+cpu_baseline = the CPU oracle timed on a bounded sample on this host.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
 import sys
@@ -34,6 +38,11 @@ CONFIGS = {
 }
 HBM_PEAK_GBS = 8000.0
 SEED = 20261201
+KERNEL_SYMBOLS = {"moe_up": "k_moe_up", "moe_down": "k_down_combine"}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def kernel_bytes(c):
@@ -48,6 +57,20 @@ def kernel_bytes(c):
     }
 
 
+def pmc_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel
+    calibration), or None when no summary for this kernel and workload exists."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    ent = data.get(workload, {}).get(KERNEL_SYMBOLS[kernel], {})
+    return int(ent["traffic_bytes"]) if "traffic_bytes" in ent else None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -57,16 +80,22 @@ def main():
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (0: config's)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-layers", type=int, default=0, help="layers in the CPU sample (0: all)")
-    ap.add_argument("--profile-steps", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU work the baseline sample aims at")
+    ap.add_argument("--profile-steps", type=int, default=8, help="replays of the event-timed step (0: skip)")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="first run a plain streaming kernel over this many MiB (PMC calibration)")
+    ap.add_argument("--rocprof-summary", metavar="DIR", help="summarise a rocprofv3 output directory and exit")
+    ap.add_argument("--pmc-out", metavar="FILE", help="with --rocprof-summary: merge PMC traffic into FILE")
     args = ap.parse_args()
 
+    if args.rocprof_summary:
+        rocprof_summary(args.rocprof_summary, args.config, args.pmc_out, args.calibrate_copy_mib)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the expert-parallel design for more GPUs is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
 
-    import numpy as np
     import torch
 
     import smoe_amd
@@ -82,8 +111,21 @@ def main():
     torch.cuda.set_stream(stream)
     ctx.set_stream(stream.cuda_stream)
 
+    if args.calibrate_copy_mib:
+        # a plain streaming kernel of known size: b = -a over N MiB of fp32
+        # reads N MiB and writes N MiB
+        n = (args.calibrate_copy_mib << 20) // 4
+        a = torch.ones(n, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(4):
+            torch.neg(a, out=b)
+        torch.cuda.synchronize()
+        del a, b
+        log(f"counter calibration: 4 x neg over {args.calibrate_copy_mib} MiB")
+
     shape = smoe_amd.make_shape(D, E, K, I)
     off, raw, stride = smoe_amd.blob_layout(D, I)
+    log(f"generating {NL} layers x {E} experts ({NL * E * stride / 1e9:.1f} GB) on the GPU")
     pool = torch.empty(NL * E * stride, dtype=torch.uint8, device=dev)
     ctx.synth_expert_pool(pool.data_ptr(), 0, NL, E, stride, shape, SEED, 0.02)
     router = torch.empty((NL, E * D), dtype=torch.int16, device=dev)
@@ -117,6 +159,7 @@ def main():
         run()
     torch.cuda.synchronize()
 
+    # timed region: K steps, synchronised on both sides
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -130,38 +173,8 @@ def main():
     elapsed = max(wall, gpu_ms / 1e3)
     ms_per_step = elapsed * 1e3 / args.steps
     tok_s = args.steps / elapsed
-
-    if args.profile_steps <= 0:
-        print(json.dumps({"value": round(tok_s, 2), "ms_per_step": round(ms_per_step, 4)}), flush=True)
-        ctx.close()
-        return
-    # per-kernel durations: HIP events around each launch on the launch stream
-    ctx.profile_enable(True)
-    for _ in range(args.profile_steps):
-        step()
-    torch.cuda.synchronize()
-    kb = kernel_bytes(c)
-    kern = {}
-    for kid, name in ((smoe_amd.KERNEL_MOE_UP, "moe_up"), (smoe_amd.KERNEL_MOE_DOWN, "moe_down")):
-        n, ms = ctx.profile_read(kid)
-        if n:
-            avg_us = ms * 1e3 / n
-            kern[name] = dict(launches=n, avg_us=round(avg_us, 3), bytes=kb[name],
-                              gbs=round(kb[name] / (avg_us * 1e-6) / 1e9, 1))
-    ctx.profile_enable(False)
-    dom = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches"])
-    layer_bytes = kb["moe_up"] + kb["moe_down"]
-    layer_us = kern["moe_up"]["avg_us"] + kern["moe_down"]["avg_us"]
-    roofline = {
-        "bound": "hbm", "kernel": dom,
-        "achieved": kern[dom]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-        "frac": round(kern[dom]["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-        "bytes_per_launch": kb[dom], "avg_us": kern[dom]["avg_us"],
-    }
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        cpu = cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, args.cpu_layers or NL)
+    log(f"timed {args.steps} steps: {ms_per_step:.4f} ms/step, {tok_s:.1f} tok/s")
+    ctx.synchronize()   # raises if a kernel reported an error (e.g. exchange time-out)
 
     line = {
         "metric": "MoE decode tok/s & achieved HBM GB/s, Qwen3-30B/235B-shaped Q4 layers",
@@ -173,64 +186,170 @@ def main():
                    "layers": NL, "batch": 1, "decode_steps": args.steps,
                    "quant": "SMOE-Q4 g64 fp16 absmax", "launch": "hip-graph" if graph else "eager",
                    "resident_expert_bytes": NL * E * raw},
-        "roofline": roofline,
-        "kernels": kern,
-        "layer_kernels_gbs": round(layer_bytes / (layer_us * 1e-6) / 1e9, 1),
-        "layer_gbs_in_stack": round((sum(kb.values())) * NL * tok_s / 1e9, 1),
-        "cpu_baseline": cpu,
     }
+
+    if args.profile_steps > 0:
+        kb = kernel_bytes(c)
+        kern, how = kernel_times(ctx, torch, stream, step, args.profile_steps)
+        for name, (n, avg_us) in kern.items():
+            kern[name] = dict(launches=n, avg_us=round(avg_us, 3), bytes=kb[name],
+                              gbs=round(kb[name] / (avg_us * 1e-6) / 1e9, 1))
+        dom = max(kern, key=lambda k: kern[k]["avg_us"] * kern[k]["launches"])
+        traffic = pmc_traffic(dom, c["workload"])
+        line["roofline"] = {
+            "bound": "hbm", "achieved": kern[dom]["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(kern[dom]["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": KERNEL_SYMBOLS[dom], "bytes_per_launch": kb[dom], "avg_us": kern[dom]["avg_us"],
+            "timing": how,
+        }
+        line["kernels"] = kern
+        layer_bytes = sum(kb.values())
+        line["layer_bytes"] = layer_bytes
+        line["stack_gbs"] = round(layer_bytes * NL * tok_s / 1e9, 1)
+
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off,
+                                            args.cpu_seconds)
     print(json.dumps(line), flush=True)
     ctx.close()
 
 
-def cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, n_layers):
-    """The oracle (CPU restatement, one thread) on one decode step through
-    n_layers layers of the same stack; each layer's weights are copied to the
-    host before its timed region.  Also reports how far the GPU's one-step
-    result is from it (layers run teacher-forced on the oracle's own state)."""
+def kernel_times(ctx, torch, stream, step, replays):
+    """Average duration of each decode kernel: the step is replayed eagerly
+    `replays` times with profiling on, so every launch carries HIP start/stop
+    events that its own dispatch records on the launch stream
+    (hipExtLaunchKernel) -- kernel execution time without launch gaps."""
+    import smoe_amd
+    ctx.profile_enable(True)
+    for _ in range(replays):
+        step()
+    torch.cuda.synchronize()
+    out = _read_profile(ctx, smoe_amd)
+    ctx.profile_enable(False)
+    return out, "hipExtLaunchKernel start/stop events on the launch stream, eager replays of the step"
+
+
+def _read_profile(ctx, smoe_amd):
+    out = {}
+    for kid, name in ((smoe_amd.KERNEL_MOE_UP, "moe_up"), (smoe_amd.KERNEL_MOE_DOWN, "moe_down")):
+        n, ms = ctx.profile_read(kid)
+        if n:
+            out[name] = (n, ms * 1e3 / n)
+    return out
+
+
+def cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, target_s):
+    """The CPU oracle (fp32 restatement, one thread) on whole decode steps of
+    the same stack, repeated until about `target_s` seconds of CPU work (at
+    least one step, at most 3 x target); host copies of the weights are made
+    before the timed region.  Also reports how far the GPU is from it on the
+    first step (layers teacher-forced on the oracle's own hidden state)."""
     import numpy as np
     import torch
+
+    import smoe_amd
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
-    D, E, K, I = c["D"], c["E"], c["K"], c["I"]
+    D, E, K, I, NL = c["D"], c["E"], c["K"], c["I"], c["layers"]
     oshape = dict(d_model=D, n_experts=E, top_k=K, d_ff=I, group_size=64, norm_topk=1)
     h_norm = norm_w.cpu().numpy().view(np.uint16)
+    layer_bytes = E * stride
+    log(f"cpu baseline: copying {NL} layers to host")
+    h_pools = [pool[l * layer_bytes:(l + 1) * layer_bytes].cpu().numpy() for l in range(NL)]
+    h_routers = [router[l].cpu().numpy().view(np.uint16) for l in range(NL)]
+
+    # parity of the GPU against the oracle on step 0, layer by layer
     h = hidden0.cpu().numpy().astype(np.float32)
     gpu_h = hidden0.clone()
-    total = 0.0
-    id_mismatch = 0
-    worst = 0.0
-    layer_bytes = E * stride
-    for l in range(n_layers):
-        h_pool = pool[l * layer_bytes:(l + 1) * layer_bytes].cpu().numpy()
-        h_router = router[l].cpu().numpy().view(np.uint16)
-        # GPU on the oracle's input (teacher forcing keeps the comparison per layer)
-        gpu_h.copy_(torch.from_numpy(h))
-        ids = torch.zeros(K, dtype=torch.int32, device="cuda")
-        lay = __import__("smoe_amd").make_layer(norm_w.data_ptr(), router[l].data_ptr(),
-                                                pool.data_ptr() + l * layer_bytes, stride, off)
-        ctx.moe_decode(shape, lay, gpu_h.data_ptr(), 1, ids.data_ptr())
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        out, oid, ow, _lg, _nr, yo = O.moe_decode_layer(oshape, h_norm, h_router, h_pool, stride, off, h)
-        total += time.perf_counter() - t0
-        g = gpu_h.cpu().numpy()
-        id_mismatch += int((ids.cpu().numpy().view(np.uint32) != oid).sum())
-        dref = (ow.astype(np.float64)[:, None] * yo.astype(np.float64)).sum(0)
-        tau = 1e-2 * np.sqrt(np.mean(dref ** 2))
-        diff = np.maximum(np.abs((g.astype(np.float64) - h) - dref) - np.spacing(np.abs(g)), 0.0)
-        worst = max(worst, float(np.max(diff / np.maximum(np.abs(dref), tau))))
-        h = out
+    ids = torch.zeros(K, dtype=torch.int32, device="cuda")
+    id_mismatch, worst = 0, 0.0
+    total, steps = 0.0, 0
+    while True:
+        for l in range(NL):
+            if steps == 0:
+                gpu_h.copy_(torch.from_numpy(h))
+                lay = smoe_amd.make_layer(norm_w.data_ptr(), router[l].data_ptr(),
+                                          pool.data_ptr() + l * layer_bytes, stride, off)
+                ctx.moe_decode(shape, lay, gpu_h.data_ptr(), 1, ids.data_ptr())
+                torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out, oid, ow, _lg, _nr, yo = O.moe_decode_layer(oshape, h_norm, h_routers[l], h_pools[l], stride,
+                                                            off, h)
+            total += time.perf_counter() - t0
+            if steps == 0:
+                g = gpu_h.cpu().numpy()
+                id_mismatch += int((ids.cpu().numpy().view(np.uint32) != oid).sum())
+                dref = (ow.astype(np.float64)[:, None] * yo.astype(np.float64)).sum(0)
+                tau = 1e-2 * np.sqrt(np.mean(dref ** 2))
+                diff = np.maximum(np.abs((g.astype(np.float64) - h) - dref) - np.spacing(np.abs(g)), 0.0)
+                worst = max(worst, float(np.max(diff / np.maximum(np.abs(dref), tau))))
+            h = out
+        steps += 1
+        log(f"cpu baseline: {steps} step(s), {total:.1f} s")
+        if total >= target_s or total * (steps + 1) / steps > 3 * target_s:
+            break
     return {
-        "value": round(1.0 / total * (n_layers / c["layers"]), 4) if total > 0 else None,
-        "unit": "tok/s", "cores": 1, "kind": "port",
-        "sample": f"1 decode step through {n_layers} of {c['layers']} layers (batch 1), oracle single thread; "
-                  f"value scaled to a full {c['layers']}-layer step; {total:.2f} s of CPU work",
+        "value": round(steps / total, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+        "sample": f"{steps} decode step(s) through all {NL} layers (batch 1), oracle on one thread, "
+                  f"{total:.1f} s of CPU work; weights copied to host before timing",
         "cpu_seconds": round(total, 3),
-        "parity_vs_gpu": {"ids_mismatch": id_mismatch, "max_rel_err_moe_delta": float(f"{worst:.3e}")},
+        "parity_vs_gpu_step0": {"ids_mismatch": id_mismatch, "max_rel_err_moe_delta": float(f"{worst:.3e}")},
     }
+
+
+# ---------------------------------------------------------------------------
+# rocprofv3 summaries (the text committed under profiles/)
+# ---------------------------------------------------------------------------
+def rocprof_summary(d, config, pmc_out, copy_mib):
+    """Print a per-kernel summary of a rocprofv3 output directory: kernel
+    stats (--kernel-trace --stats) and, for --pmc runs, the average counter
+    value per dispatch of each kernel.  With --pmc-out (and the size given by
+    --calibrate-copy-mib), FETCH_SIZE/WRITE_SIZE averages of the decode kernels
+    are scaled by expected/measured of the same counter for the calibration
+    kernel (b = -a over that many MiB: reads and writes exactly that much) and
+    merged into that JSON file."""
+    for p in sorted(glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)):
+        print(f"== {os.path.basename(p)}")
+        print(f"{'calls':>7} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'pct':>6}  kernel")
+        for r in csv.DictReader(open(p)):
+            print(f"{int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.3f} {float(r['MinNs']) / 1e3:9.3f} "
+                  f"{float(r['MaxNs']) / 1e3:9.3f} {float(r['Percentage']):6.2f}  {r['Name'][:90]}")
+    acc = {}
+    for p in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
+        for r in csv.DictReader(open(p)):
+            s = acc.setdefault((r["Kernel_Name"], r["Counter_Name"]), [0.0, 0])
+            s[0] += float(r["Counter_Value"])
+            s[1] += 1
+    if not acc:
+        return
+    print("== counters (average per dispatch)")
+    for (k, cn), (tot, n) in sorted(acc.items()):
+        print(f"{cn:>12} {tot / n:14.1f}  n={n:5d}  {k[:90]}")
+    if not (pmc_out and copy_mib):
+        return
+    data = json.load(open(pmc_out)) if os.path.exists(pmc_out) else {}
+    ent = data.setdefault(CONFIGS[config]["workload"], {})
+    for cn in ("FETCH_SIZE", "WRITE_SIZE"):
+        copies = [tot / n for (k, c2), (tot, n) in acc.items() if c2 == cn and "neg_kernel" in k]
+        if not copies:
+            continue
+        copy_kib = max(copies)
+        scale = copy_mib * 1024.0 / copy_kib        # expected KiB / measured KiB for the copy
+        data.setdefault("_calibration", {})[cn] = {"copy_mib": copy_mib, "copy_kib_measured": round(copy_kib, 1),
+                                                    "scale": round(scale, 4)}
+        for sym in KERNEL_SYMBOLS.values():
+            vals = [tot / n for (k, c2), (tot, n) in acc.items() if c2 == cn and sym in k]
+            if vals:
+                e = ent.setdefault(sym, {})
+                e[cn + "_kib"] = round(vals[0], 1)
+                e[cn + "_bytes_scaled"] = int(vals[0] * 1024 * scale)
+                if "FETCH_SIZE_bytes_scaled" in e and "WRITE_SIZE_bytes_scaled" in e:
+                    e["traffic_bytes"] = e["FETCH_SIZE_bytes_scaled"] + e["WRITE_SIZE_bytes_scaled"]
+    with open(pmc_out, "w") as f:
+        json.dump(data, f, indent=1, sort_keys=True)
+    print(f"== merged into {pmc_out}")
 
 
 if __name__ == "__main__":

@@ -212,8 +212,9 @@ void prof_flush_slot(SmoeMetalCtx* ctx, SmoeMetalCtx::ProfSlot& p)
     p.pending = false;
 }
 
-// bracket one kernel launch with timing events (no-op unless profiling and
-// the stream is not being captured)
+// Time one kernel launch (no-op unless profiling; skipped under stream
+// capture): the slot's events are handed to the launcher, which records them
+// at the dispatch's own start and end.
 void prof_begin(SmoeMetalCtx* ctx, uint32_t kind)
 {
     ctx->prof_open = -1;
@@ -222,17 +223,16 @@ void prof_begin(SmoeMetalCtx* ctx, uint32_t kind)
     auto& p = ctx->prof[i];
     prof_flush_slot(ctx, p);
     p.kind = kind;
-    if (hipEventRecord(p.a, ctx->stream) == hipSuccess) ctx->prof_open = static_cast<int>(i);
+    smoe::dispatch_timer() = smoe::DispatchTimer{p.a, p.b};
+    ctx->prof_open = static_cast<int>(i);
 }
 
 void prof_end(SmoeMetalCtx* ctx)
 {
     if (ctx->prof_open < 0) return;
-    auto& p = ctx->prof[ctx->prof_open];
-    if (hipEventRecord(p.b, ctx->stream) == hipSuccess) {
-        p.pending = true;
-        ctx->prof_head++;
-    }
+    smoe::dispatch_timer() = smoe::DispatchTimer{};
+    ctx->prof[ctx->prof_open].pending = true;
+    ctx->prof_head++;
     ctx->prof_open = -1;
 }
 

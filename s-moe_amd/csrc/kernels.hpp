@@ -2,6 +2,7 @@
 // libsmoe_hip.so; the public surface is include/smoe_hip.h).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -10,6 +11,27 @@ namespace smoe {
 // largest expert count a top-k wave handles (8 positions per lane)
 constexpr int SMOE_TOPK_MAX_N = 512;
 constexpr int SMOE_TOPK_MAX_K = 16;
+
+// Events that time the next kernel dispatches of this thread: when set, the
+// launchers dispatch through hipExtLaunchKernel, which records `start` when
+// the kernel begins executing and `stop` when it completes (the dispatch's
+// own timestamps, no marker packets around it).  Set only around eager
+// launches by the profiling path of the C ABI.
+struct DispatchTimer {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+DispatchTimer& dispatch_timer();
+
+template <typename... KArgs, typename... Args>
+inline void launch_kernel(void (*k)(KArgs...), dim3 grid, dim3 block, hipStream_t s, Args... args)
+{
+    const DispatchTimer& t = dispatch_timer();
+    if (t.start)
+        hipExtLaunchKernelGGL(k, grid, block, 0, s, t.start, t.stop, 0, static_cast<KArgs>(args)...);
+    else
+        hipLaunchKernelGGL(k, grid, block, 0, s, static_cast<KArgs>(args)...);
+}
 
 // Routing exchange of one token: LL_COPIES copies of its E logit words (flag
 // in the high half), ll_copy_words(E) words apart (> 4 KB), so the waves that

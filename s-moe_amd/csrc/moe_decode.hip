@@ -28,6 +28,12 @@
 
 namespace smoe {
 
+DispatchTimer& dispatch_timer()
+{
+    static thread_local DispatchTimer t;
+    return t;
+}
+
 // ---------------------------------------------------------------------------
 // softmax + selection sort with swaps (scout.cpp:77-123) in one wave.
 // Round s scans positions s..n-1 with a strict '>' and swaps the winner into
@@ -660,9 +666,9 @@ static void moe_up_c(dim3 grid, hipStream_t s, const MoeDims& d, const LayerDesc
                      uint64_t* ll, float* h, uint32_t* ids, float* w, ExpertPtrs* tbl, uint32_t* err)
 {
     if (d.E <= 128)
-        hipLaunchKernelGGL((k_moe_up<CPL, 2>), grid, dim3(WAVE), 0, s, d, L, hidden, ll, h, ids, w, tbl, err);
+        launch_kernel(k_moe_up<CPL, 2>, grid, dim3(WAVE), s, d, L, hidden, ll, h, ids, w, tbl, err);
     else
-        hipLaunchKernelGGL((k_moe_up<CPL, 8>), grid, dim3(WAVE), 0, s, d, L, hidden, ll, h, ids, w, tbl, err);
+        launch_kernel(k_moe_up<CPL, 8>, grid, dim3(WAVE), s, d, L, hidden, ll, h, ids, w, tbl, err);
 }
 
 hipError_t launch_moe_up(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t n_tok, uint64_t* ll,
@@ -683,9 +689,9 @@ hipError_t launch_topk(const float* scores, uint32_t rows, uint32_t n, uint32_t 
                        uint32_t norm, uint32_t* ids, float* w, hipStream_t s)
 {
     if (topk_vpl(n) == 2)
-        hipLaunchKernelGGL(k_topk<2>, dim3(rows), dim3(WAVE), 0, s, scores, n, k, norm, ids, w);
+        launch_kernel(k_topk<2>, dim3(rows), dim3(WAVE), s, scores, n, k, norm, ids, w);
     else
-        hipLaunchKernelGGL(k_topk<8>, dim3(rows), dim3(WAVE), 0, s, scores, n, k, norm, ids, w);
+        launch_kernel(k_topk<8>, dim3(rows), dim3(WAVE), s, scores, n, k, norm, ids, w);
     return hipGetLastError();
 }
 
@@ -704,7 +710,7 @@ static hipError_t launch_rows(const MoeDims& d, const ExpertPtrs* tbl, uint32_t 
     dim3 grid((waves + 3) / 4, n_tok);
 #define SMOE_ROWS_CASE(C)                                                                     \
     case C:                                                                                    \
-        hipLaunchKernelGGL((k_q4_rows<C, RB, GATE_UP>), grid, dim3(256), 0, s, d, tbl, n_exp,  \
+        launch_kernel(k_q4_rows<C, RB, GATE_UP>, grid, dim3(256), s, d, tbl, n_exp,  \
                            x, x_slot_stride, out, out_stride, x_tok_stride, tbl_tok_stride,    \
                            out_tok_stride);                                                    \
         break;
@@ -748,9 +754,9 @@ hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const fl
     if (nw > DOWN_MAX_WAVES || d.D % DOWN_RB) return hipErrorInvalidValue;
     dim3 grid(d.D / DOWN_RB, n_tok), block(nw * WAVE);
     switch (ppl) {
-        case 1: hipLaunchKernelGGL(k_down_combine<1>, grid, block, 0, s, d, tbl, h, w, hidden, ll); break;
-        case 2: hipLaunchKernelGGL(k_down_combine<2>, grid, block, 0, s, d, tbl, h, w, hidden, ll); break;
-        default: hipLaunchKernelGGL(k_down_combine<4>, grid, block, 0, s, d, tbl, h, w, hidden, ll); break;
+        case 1: launch_kernel(k_down_combine<1>, grid, block, s, d, tbl, h, w, hidden, ll); break;
+        case 2: launch_kernel(k_down_combine<2>, grid, block, s, d, tbl, h, w, hidden, ll); break;
+        default: launch_kernel(k_down_combine<4>, grid, block, s, d, tbl, h, w, hidden, ll); break;
     }
     return hipGetLastError();
 }
