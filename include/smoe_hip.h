@@ -163,8 +163,10 @@ typedef struct {
  * of its own.  No synchronisation is implied. */
 int smoe_hip_set_stream(SmoeMetalCtx* ctx, void* hip_stream);
 
-/* Synchronise the context's stream; also reports (SMOE_ERR_HIP) a timed-out
- * routing exchange inside smoe_hip_moe_decode. */
+/* Synchronise the context's stream and report the device-side error flags
+ * raised since the last call, then clear them: a timed-out routing exchange
+ * inside smoe_hip_moe_decode (SMOE_ERR_HIP) or an expert id >= n_experts
+ * given to smoe_hip_permute (SMOE_ERR_ARG). */
 int smoe_hip_synchronize(SmoeMetalCtx* ctx);
 
 /* Reserve device scratch for layers of this shape and up to max_tokens tokens
@@ -184,9 +186,14 @@ int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
                         const SmoeMoeLayer* layer, float* hidden, uint32_t n_tokens,
                         uint32_t* ids_out, float* weights_out);
 
-/* Prefill MoE block (prefill.cpp:308-453) over n_tokens rows: the same math
- * with the layer-major expert grouping (permute by expert, grouped GEMM,
- * weighted scatter).  Optional device outputs of the permute:
+/* Prefill MoE block (prefill.cpp:308-453) over n_tokens rows [n_tokens x
+ * d_model]: per token RMSNorm + router + top-k, then the layer-major expert
+ * grouping (token-by-expert permute, grouped expert GEMMs on MFMA, weighted
+ * combine into the residual).  Tokens are processed in passes of as many as
+ * one permute workgroup holds (736 at 128 experts x top-8); results do not
+ * depend on the pass size.  ids_out / weights_out [n_tokens x top_k] are
+ * optional.  Optional device outputs of the permute (these require all tokens
+ * in one pass, else SMOE_ERR_SHAPE):
  *   expert_offsets [n_experts+1], sorted_tokens [n_tokens*top_k],
  *   union_ids [n_experts] (first-appearance order, prefill.cpp:55-68),
  *   union_size [1]. */
@@ -203,10 +210,13 @@ int smoe_hip_compute_top_k(SmoeMetalCtx* ctx, const float* scores, uint32_t n_ro
                            int norm_topk);
 
 /* Token-by-expert permute (prefill.cpp:38-68, :315-332) of ids [n_tokens x
- * top_k] on device: stable counting sort of (token, rank) pairs by expert.
- * expert_offsets [n_experts+1]; sorted_tokens / sorted_weights [n_tokens*top_k]
- * (ascending token order inside each expert); union_ids [n_experts] in order
- * of first appearance; union_size [1]. */
+ * top_k] on device: stable counting sort of (token, rank) pairs by expert, in
+ * one workgroup (n_tokens*top_k up to ~5900 pairs at 128 experts; larger
+ * inputs return SMOE_ERR_SHAPE).  expert_offsets [n_experts+1] (required);
+ * sorted_tokens / sorted_weights [n_tokens*top_k] (ascending token order
+ * inside each expert); union_ids [n_experts] in order of first appearance;
+ * union_size [1] -- all optional.  Ids >= n_experts are skipped and reported
+ * by the next smoe_hip_synchronize. */
 int smoe_hip_permute(SmoeMetalCtx* ctx, const uint32_t* ids, const float* weights,
                      uint32_t n_tokens, uint32_t top_k, uint32_t n_experts,
                      uint32_t* expert_offsets, uint32_t* sorted_tokens,
@@ -247,7 +257,9 @@ int smoe_hip_synth_expert_pool(SmoeMetalCtx* ctx, uint8_t* base, uint32_t first_
 #define SMOE_KERNEL_PERMUTE       5
 #define SMOE_KERNEL_GROUPED_GATE_UP 6
 #define SMOE_KERNEL_GROUPED_DOWN  7
-#define SMOE_KERNEL_SCATTER       8
+#define SMOE_KERNEL_SCATTER       8   /* prefill: weighted combine of pair outputs + residual */
+#define SMOE_KERNEL_ROUTE         9   /* prefill: RMSNorm + router + top-k per token          */
+#define SMOE_KERNEL_SPLIT        10   /* prefill: f16 hi/lo planes of activations             */
 #define SMOE_KERNEL_KINDS        16
 int smoe_hip_profile_enable(SmoeMetalCtx* ctx, int enable);
 int smoe_hip_profile_read(SmoeMetalCtx* ctx, uint32_t kernel, uint64_t* launches, double* total_ms);

@@ -30,11 +30,28 @@ struct DeviceScratch {
     // capacities
     uint32_t D = 0, E = 0, K = 0, I = 0, T = 0;
     uint64_t* ll = nullptr;      // [T x ll_token_words(E)] routing exchange words
-    uint32_t* err = nullptr;     // [1] device-side error flags
     uint32_t* ids = nullptr;     // [T x K]
     float* w = nullptr;          // [T x K]
     ExpertPtrs* tbl = nullptr;   // [T x K]
     float* h = nullptr;          // [T x K x I]
+};
+
+// prefill / permute scratch for one batch of up to T tokens (P = T * K pairs)
+struct PrefillScratch {
+    uint32_t D = 0, E = 0, K = 0, I = 0, T = 0;
+    float* normed = nullptr;        // [T x D]
+    uint16_t* x_hi = nullptr;       // [T x D] f16
+    uint16_t* x_lo = nullptr;
+    float2* x_st = nullptr;         // [T x D/64]
+    uint32_t* ids = nullptr;        // [T x K]
+    float* w = nullptr;             // [T x K]
+    uint32_t* offsets = nullptr;    // [E + 1]
+    uint32_t* pairs = nullptr;      // [P] sorted pair ids
+    float* h = nullptr;             // [P x I]
+    uint16_t* h_hi = nullptr;       // [P x I] f16
+    uint16_t* h_lo = nullptr;
+    float2* h_st = nullptr;         // [P x I/64]
+    float* y = nullptr;             // [P x D]
 };
 
 }  // namespace
@@ -60,6 +77,10 @@ struct SmoeMetalCtx {
     std::atomic<uint64_t> dispatches{0};
 
     DeviceScratch ds;
+    PrefillScratch ps;
+    uint32_t* d_err = nullptr;       // [1] device-side error flags (bit 0: exchange time-out, bit 1: bad expert id)
+    uint32_t* perm_pairs = nullptr;  // smoe_hip_permute's sorted pair ids
+    uint64_t perm_cap = 0;
     std::vector<std::pair<uintptr_t, size_t>> registered;
     char last_err[256] = {0};
 
@@ -105,12 +126,29 @@ void dfree(T*& p)
 void free_device_scratch(DeviceScratch& s)
 {
     dfree(s.ll);
-    dfree(s.err);
     dfree(s.ids);
     dfree(s.w);
     dfree(s.tbl);
     dfree(s.h);
     s = DeviceScratch{};
+}
+
+void free_prefill_scratch(PrefillScratch& s)
+{
+    dfree(s.normed);
+    dfree(s.x_hi);
+    dfree(s.x_lo);
+    dfree(s.x_st);
+    dfree(s.ids);
+    dfree(s.w);
+    dfree(s.offsets);
+    dfree(s.pairs);
+    dfree(s.h);
+    dfree(s.h_hi);
+    dfree(s.h_lo);
+    dfree(s.h_st);
+    dfree(s.y);
+    s = PrefillScratch{};
 }
 
 // reference-surface shape check (kernels.metal:146-152, metal_bridge.mm:460-461)
@@ -186,13 +224,53 @@ int ensure_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
     n.T = std::max(c.T, T);
     free_device_scratch(c);
     const size_t T_ = n.T;
-    bool ok = dalloc(ctx, &n.ll, T_ * smoe::ll_token_words(n.E)) && dalloc(ctx, &n.err, 1) && dalloc(ctx, &n.ids, T_ * n.K) &&
+    bool ok = dalloc(ctx, &n.ll, T_ * smoe::ll_token_words(n.E)) && dalloc(ctx, &n.ids, T_ * n.K) &&
               dalloc(ctx, &n.w, T_ * n.K) && dalloc(ctx, &n.tbl, T_ * n.K) && dalloc(ctx, &n.h, T_ * n.K * n.I);
     // the exchange words start disarmed; every launch pair leaves them so
-    ok = ok && hip_ok(ctx, hipMemset(n.ll, 0, T_ * smoe::ll_token_words(n.E) * sizeof(uint64_t)), "hipMemset") &&
-         hip_ok(ctx, hipMemset(n.err, 0, sizeof(uint32_t)), "hipMemset");
+    ok = ok && hip_ok(ctx, hipMemset(n.ll, 0, T_ * smoe::ll_token_words(n.E) * sizeof(uint64_t)), "hipMemset");
     if (!ok) {
         free_device_scratch(n);
+        return SMOE_ERR_HIP;
+    }
+    c = n;
+    return SMOE_OK;
+}
+
+// largest token batch of one prefill pass: the permute's per-(chunk, expert)
+// counts live in one workgroup's LDS
+uint32_t prefill_max_tokens(uint32_t E, uint32_t K)
+{
+    uint32_t lo = 1, hi = 1u << 16;
+    if (smoe::permute_lds_bytes(K, E) > smoe::PERMUTE_MAX_LDS) return 0;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi + 1) / 2;
+        if (smoe::permute_lds_bytes(mid * K, E) <= smoe::PERMUTE_MAX_LDS) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+int ensure_prefill_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
+{
+    PrefillScratch& c = ctx->ps;
+    if (c.normed && c.D >= s->d_model && c.E >= s->n_experts && c.K >= s->top_k && c.I >= s->d_ff && c.T >= T)
+        return SMOE_OK;
+    if (stream_capturing(ctx->stream)) return SMOE_ERR_CAPTURE;
+    if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
+    PrefillScratch n;
+    n.D = std::max(c.D, s->d_model);
+    n.E = std::max(c.E, s->n_experts);
+    n.K = std::max(c.K, s->top_k);
+    n.I = std::max(c.I, s->d_ff);
+    n.T = std::max(c.T, T);
+    free_prefill_scratch(c);
+    const size_t T_ = n.T, P = T_ * n.K;
+    const bool ok = dalloc(ctx, &n.normed, T_ * n.D) && dalloc(ctx, &n.x_hi, T_ * n.D) &&
+                    dalloc(ctx, &n.x_lo, T_ * n.D) && dalloc(ctx, &n.x_st, T_ * n.D / 64) &&
+                    dalloc(ctx, &n.ids, P) && dalloc(ctx, &n.w, P) && dalloc(ctx, &n.offsets, size_t(n.E) + 1) &&
+                    dalloc(ctx, &n.pairs, P) && dalloc(ctx, &n.h, P * n.I) && dalloc(ctx, &n.h_hi, P * n.I) &&
+                    dalloc(ctx, &n.h_lo, P * n.I) && dalloc(ctx, &n.h_st, P * n.I / 64) && dalloc(ctx, &n.y, P * n.D);
+    if (!ok) {
+        free_prefill_scratch(n);
         return SMOE_ERR_HIP;
     }
     c = n;
@@ -309,7 +387,8 @@ extern "C" SmoeMetalCtx* smoe_metal_init(size_t slot_bytes)
               dalloc(ctx, &ctx->d_input, SMOE_MAX_DIM) && dalloc(ctx, &ctx->d_hidden, size_t(kSlots) * ctx->max_rows) &&
               dalloc(ctx, &ctx->d_output, size_t(kSlots) * ctx->max_rows) && dalloc(ctx, &ctx->d_batch_in, plane) &&
               dalloc(ctx, &ctx->d_batch_hidden, plane) && dalloc(ctx, &ctx->d_batch_out, plane) &&
-              dalloc(ctx, &ctx->d_tbl_ref, kSlots);
+              dalloc(ctx, &ctx->d_tbl_ref, kSlots) && dalloc(ctx, &ctx->d_err, 1) &&
+              hip_ok(ctx, hipMemset(ctx->d_err, 0, sizeof(uint32_t)), "hipMemset");
     for (uint32_t i = 0; ok && i < kEvents; ++i)
         ok = hip_ok(ctx, hipEventCreateWithFlags(&ctx->ev[i], hipEventDisableTiming), "hipEventCreate");
     if (!ok) {
@@ -326,6 +405,9 @@ extern "C" void smoe_metal_destroy(SmoeMetalCtx* ctx)
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->own_stream && ctx->own_stream != ctx->stream) (void)hipStreamSynchronize(ctx->own_stream);
     free_device_scratch(ctx->ds);
+    free_prefill_scratch(ctx->ps);
+    dfree(ctx->perm_pairs);
+    dfree(ctx->d_err);
     dfree(ctx->d_input);
     dfree(ctx->d_hidden);
     dfree(ctx->d_output);
@@ -473,13 +555,16 @@ extern "C" int smoe_hip_synchronize(SmoeMetalCtx* ctx)
 {
     if (!ctx) return SMOE_ERR_ARG;
     if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
-    if (ctx->ds.err) {
+    if (ctx->d_err) {
         uint32_t e = 0;
-        if (!hip_ok(ctx, hipMemcpy(&e, ctx->ds.err, sizeof(e), hipMemcpyDeviceToHost), "hipMemcpy(err)"))
+        if (!hip_ok(ctx, hipMemcpy(&e, ctx->d_err, sizeof(e), hipMemcpyDeviceToHost), "hipMemcpy(err)"))
             return SMOE_ERR_HIP;
         if (e) {
-            std::snprintf(ctx->last_err, sizeof(ctx->last_err), "device: routing exchange timed out (flags %u)", e);
-            return SMOE_ERR_HIP;
+            // reported once: clear for the next call
+            if (!hip_ok(ctx, hipMemset(ctx->d_err, 0, sizeof(uint32_t)), "hipMemset(err)")) return SMOE_ERR_HIP;
+            std::snprintf(ctx->last_err, sizeof(ctx->last_err), "device:%s%s (flags %u)",
+                          (e & 1u) ? " routing exchange timed out" : "", (e & 2u) ? " expert id out of range" : "", e);
+            return (e & 1u) ? SMOE_ERR_HIP : SMOE_ERR_ARG;
         }
     }
     return SMOE_OK;
@@ -508,7 +593,7 @@ static int moe_forward(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, const SmoeM
     uint32_t* ids = ids_out ? ids_out : s.ids;
     float* w = weights_out ? weights_out : s.w;
     if (!timed(ctx, SMOE_KERNEL_MOE_UP, "moe_up", [&] {
-            return smoe::launch_moe_up(d, L, hidden, n_tokens, s.ll, s.h, ids, w, s.tbl, s.err, ctx->stream);
+            return smoe::launch_moe_up(d, L, hidden, n_tokens, s.ll, s.h, ids, w, s.tbl, ctx->d_err, ctx->stream);
         }))
         return SMOE_ERR_HIP;
     if (!timed(ctx, SMOE_KERNEL_MOE_DOWN, "moe_down",
@@ -529,11 +614,50 @@ extern "C" int smoe_hip_moe_prefill(SmoeMetalCtx* ctx, const SmoeMoeShape* shape
                                     uint32_t* expert_offsets, uint32_t* sorted_tokens, uint32_t* union_ids,
                                     uint32_t* union_size)
 {
-    (void)expert_offsets;
-    (void)sorted_tokens;
-    (void)union_ids;
-    (void)union_size;
-    return moe_forward(ctx, shape, layer, hidden, n_tokens, ids_out, weights_out);
+    if (!ctx || !shape || !layer || !hidden || n_tokens == 0) return SMOE_ERR_ARG;
+    if (!layer->norm_w || !layer->router_w || !layer->experts) return SMOE_ERR_ARG;
+    int rc = shape_check(shape);
+    if (rc != SMOE_OK) return rc;
+    const MoeDims d = dims_of(shape);
+    const LayerDesc L = layer_of(layer);
+    const uint32_t tmax = prefill_max_tokens(d.E, d.K);
+    if (tmax == 0) return SMOE_ERR_SHAPE;
+    // the permute outputs describe one pass: they need all tokens in one batch
+    const bool want_perm = expert_offsets || sorted_tokens || union_ids || union_size;
+    if (want_perm && n_tokens > tmax) return SMOE_ERR_SHAPE;
+    const uint32_t tb = std::min(n_tokens, tmax);
+    rc = ensure_prefill_scratch(ctx, shape, tb);
+    if (rc != SMOE_OK) return rc;
+    PrefillScratch& s = ctx->ps;
+    hipStream_t st = ctx->stream;
+    for (uint32_t t0 = 0; t0 < n_tokens; t0 += tb) {
+        const uint32_t T = std::min(tb, n_tokens - t0), P = T * d.K;
+        float* hv = hidden + size_t(t0) * d.D;
+        uint32_t* ids = ids_out ? ids_out + size_t(t0) * d.K : s.ids;
+        float* w = weights_out ? weights_out + size_t(t0) * d.K : s.w;
+        uint32_t* offs = expert_offsets ? expert_offsets : s.offsets;
+        if (!timed(ctx, SMOE_KERNEL_ROUTE, "route",
+                   [&] { return smoe::launch_route(d, L, hv, T, s.normed, ids, w, st); }) ||
+            !timed(ctx, SMOE_KERNEL_SPLIT, "split(x)",
+                   [&] { return smoe::launch_split_rows(s.normed, T, d.D, s.x_hi, s.x_lo, s.x_st, st); }) ||
+            !timed(ctx, SMOE_KERNEL_PERMUTE, "permute", [&] {
+                return smoe::launch_permute(ids, w, P, d.K, d.E, offs, s.pairs, sorted_tokens, nullptr, union_ids,
+                                            union_size, ctx->d_err, st);
+            }) ||
+            !timed(ctx, SMOE_KERNEL_GROUPED_GATE_UP, "grouped_gate_up", [&] {
+                return smoe::launch_grouped_gate_up(d, L, offs, s.pairs, s.x_hi, s.x_lo, s.x_st, s.h, st);
+            }) ||
+            !timed(ctx, SMOE_KERNEL_SPLIT, "split(h)",
+                   [&] { return smoe::launch_split_rows(s.h, P, d.I, s.h_hi, s.h_lo, s.h_st, st); }) ||
+            !timed(ctx, SMOE_KERNEL_GROUPED_DOWN, "grouped_down", [&] {
+                return smoe::launch_grouped_down(d, L, offs, s.pairs, s.h_hi, s.h_lo, s.h_st, s.y, st);
+            }) ||
+            !timed(ctx, SMOE_KERNEL_SCATTER, "combine",
+                   [&] { return smoe::launch_combine_pairs(s.y, w, T, d.K, d.D, hv, st); }))
+            return SMOE_ERR_HIP;
+        ctx->dispatches.fetch_add(uint64_t(P), std::memory_order_relaxed);
+    }
+    return SMOE_OK;
 }
 
 extern "C" int smoe_hip_compute_top_k(SmoeMetalCtx* ctx, const float* scores, uint32_t n_rows, uint32_t n,
@@ -552,18 +676,29 @@ extern "C" int smoe_hip_permute(SmoeMetalCtx* ctx, const uint32_t* ids, const fl
                                 uint32_t* sorted_tokens, float* sorted_weights, uint32_t* union_ids,
                                 uint32_t* union_size)
 {
-    (void)ids;
-    (void)weights;
-    (void)n_tokens;
-    (void)top_k;
-    (void)n_experts;
-    (void)expert_offsets;
-    (void)sorted_tokens;
-    (void)sorted_weights;
-    (void)union_ids;
-    (void)union_size;
-    if (!ctx) return SMOE_ERR_ARG;
-    return SMOE_ERR_SHAPE;
+    if (!ctx || !ids || !expert_offsets || n_tokens == 0 || top_k == 0 || n_experts == 0) return SMOE_ERR_ARG;
+    if (sorted_weights && !weights) return SMOE_ERR_ARG;
+    if (top_k > SMOE_MAX_ACTIVE || n_experts > SMOE_MAX_EXPERTS) return SMOE_ERR_SHAPE;
+    const uint64_t P = uint64_t(n_tokens) * top_k;
+    if (P > 0xFFFFFFFFull || smoe::permute_lds_bytes(static_cast<uint32_t>(P), n_experts) > smoe::PERMUTE_MAX_LDS)
+        return SMOE_ERR_SHAPE;
+    // scratch for the sorted pair ids
+    if (!ctx->perm_pairs || ctx->perm_cap < P) {
+        if (stream_capturing(ctx->stream)) return SMOE_ERR_CAPTURE;
+        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
+        dfree(ctx->perm_pairs);
+        ctx->perm_cap = 0;
+        if (!dalloc(ctx, &ctx->perm_pairs, P)) return SMOE_ERR_HIP;
+        ctx->perm_cap = P;
+    }
+    return timed(ctx, SMOE_KERNEL_PERMUTE, "permute",
+                 [&] {
+                     return smoe::launch_permute(ids, weights, static_cast<uint32_t>(P), top_k, n_experts,
+                                                 expert_offsets, ctx->perm_pairs, sorted_tokens, sorted_weights,
+                                                 union_ids, union_size, ctx->d_err, ctx->stream);
+                 })
+               ? SMOE_OK
+               : SMOE_ERR_HIP;
 }
 
 extern "C" int smoe_hip_quantize_q4(SmoeMetalCtx* ctx, const float* w, uint64_t n, uint32_t group_size,

@@ -24,13 +24,19 @@ struct DispatchTimer {
 DispatchTimer& dispatch_timer();
 
 template <typename... KArgs, typename... Args>
-inline void launch_kernel(void (*k)(KArgs...), dim3 grid, dim3 block, hipStream_t s, Args... args)
+inline void launch_kernel_lds(void (*k)(KArgs...), dim3 grid, dim3 block, uint32_t lds, hipStream_t s, Args... args)
 {
     const DispatchTimer& t = dispatch_timer();
     if (t.start)
-        hipExtLaunchKernelGGL(k, grid, block, 0, s, t.start, t.stop, 0, static_cast<KArgs>(args)...);
+        hipExtLaunchKernelGGL(k, grid, block, lds, s, t.start, t.stop, 0, static_cast<KArgs>(args)...);
     else
-        hipLaunchKernelGGL(k, grid, block, 0, s, static_cast<KArgs>(args)...);
+        hipLaunchKernelGGL(k, grid, block, lds, s, static_cast<KArgs>(args)...);
+}
+
+template <typename... KArgs, typename... Args>
+inline void launch_kernel(void (*k)(KArgs...), dim3 grid, dim3 block, hipStream_t s, Args... args)
+{
+    launch_kernel_lds(k, grid, block, 0u, s, args...);
 }
 
 // Routing exchange of one token: LL_COPIES copies of its E logit words (flag
@@ -89,6 +95,35 @@ hipError_t launch_down_slots(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n
 // softmax + top-k over rows of scores (scout.cpp:77-123)
 hipError_t launch_topk(const float* scores, uint32_t rows, uint32_t n, uint32_t k,
                        uint32_t norm, uint32_t* ids, float* w, hipStream_t s);
+
+
+// ---- prefill, T token rows (moe_prefill.hip) -----------------------------
+// RMSNorm + router + top-k for T tokens: normed [T x D], ids/w [T x K].
+hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, float* normed,
+                        uint32_t* ids, float* w, hipStream_t s);
+// Per (row, 64-column group) of src [rows x cols]: f16 hi/lo planes of
+// x * 2^-e (|x| < 2^e) and st = (sum of hi + lo, 2^e).
+hipError_t launch_split_rows(const float* src, uint32_t rows, uint32_t cols, uint16_t* hi, uint16_t* lo,
+                             float2* st, hipStream_t s);
+// Stable counting sort of the P pairs by expert: offsets [E+1],
+// sorted_pairs [P] (pair = token * K + rank); sorted_tokens, sorted_w,
+// union_ids [E], union_size [1] optional (nullptr).  Bad ids set err bit 1.
+constexpr size_t PERMUTE_MAX_LDS = 48 * 1024;
+size_t permute_lds_bytes(uint32_t P, uint32_t E);
+hipError_t launch_permute(const uint32_t* ids, const float* w, uint32_t P, uint32_t K, uint32_t E, uint32_t* offsets,
+                          uint32_t* sorted_pairs, uint32_t* sorted_tokens, float* sorted_w, uint32_t* union_ids,
+                          uint32_t* union_size, uint32_t* err, hipStream_t s);
+// Grouped expert GEMMs over the permuted pairs (MFMA f16, hi/lo activations):
+// h [P x I] = silu(x G^T) * (x U^T); y [P x D] = h Dn^T.
+hipError_t launch_grouped_gate_up(const MoeDims& d, const LayerDesc& L, const uint32_t* offsets,
+                                  const uint32_t* sorted_pairs, const uint16_t* x_hi, const uint16_t* x_lo,
+                                  const float2* x_st, float* h, hipStream_t s);
+hipError_t launch_grouped_down(const MoeDims& d, const LayerDesc& L, const uint32_t* offsets,
+                               const uint32_t* sorted_pairs, const uint16_t* h_hi, const uint16_t* h_lo,
+                               const float2* h_st, float* y, hipStream_t s);
+// hidden[t] += sum_r w[t][r] * y[t*K + r] (rank order).
+hipError_t launch_combine_pairs(const float* y, const float* w, uint32_t T, uint32_t K, uint32_t D, float* hidden,
+                                hipStream_t s);
 
 // ---- synthetic generator / quantizer (synth.hip) -------------------------
 hipError_t launch_synth_normal(float* out, uint64_t n, uint64_t seed, uint64_t stream,

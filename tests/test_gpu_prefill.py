@@ -1,0 +1,176 @@
+"""GPU parity of the prefill path (prefill.cpp:308-453) against the CPU oracle:
+the token-by-expert permute bit-exact (orc_permute, prefill.cpp:38-68), the
+router top-k ids bit-exact, the hidden update within 1e-3 (relative error per
+element with a floor of 1% of the delta's RMS)."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import Layer, hidden_states, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def gpu_permute(ctx, ids, w, E):
+    T, K = ids.shape
+    d_ids = torch.from_numpy(ids.astype(np.int32)).cuda()
+    d_w = torch.from_numpy(w.astype(np.float32)).cuda()
+    offs = torch.zeros(E + 1, dtype=torch.int32, device="cuda")
+    tok = torch.full((T * K,), -1, dtype=torch.int32, device="cuda")
+    wo = torch.zeros(T * K, dtype=torch.float32, device="cuda")
+    uni = torch.full((E,), -1, dtype=torch.int32, device="cuda")
+    nu = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ctx.permute(d_ids.data_ptr(), d_w.data_ptr(), T, K, E, offs.data_ptr(), tok.data_ptr(), wo.data_ptr(),
+                uni.data_ptr(), nu.data_ptr())
+    ctx.synchronize()
+    n = int(nu.item())
+    return (offs.cpu().numpy().view(np.uint32), tok.cpu().numpy().view(np.uint32), wo.cpu().numpy(),
+            uni.cpu().numpy().view(np.uint32)[:n])
+
+
+@pytest.mark.parametrize("T,K,E,kind", [
+    (512, 8, 128, "random"), (1, 8, 128, "random"), (37, 4, 16, "random"), (64, 8, 128, "one_expert"),
+    (200, 6, 7, "random"), (736, 8, 128, "zipf"), (60, 16, 512, "random"),
+])
+def test_permute_bit_exact(ctx, oracle, T, K, E, kind):
+    rng = np.random.default_rng(T * 7 + K)
+    if kind == "one_expert":
+        ids = np.full((T, K), 5, np.uint32)
+    elif kind == "zipf":
+        p = 1.0 / np.arange(1, E + 1) ** 1.1
+        ids = rng.choice(E, size=(T, K), p=p / p.sum()).astype(np.uint32)
+    else:
+        ids = np.stack([rng.choice(E, size=K, replace=K > E) for _ in range(T)]).astype(np.uint32)
+    w = rng.random((T, K), dtype=np.float32)
+    go, gt, gw, gu = gpu_permute(ctx, ids, w, E)
+    ro, rt, rw, ru = oracle.permute(ids, w, E)
+    assert (go == ro).all()
+    assert (gt == rt).all()
+    assert (gw == rw).all()
+    assert (gu == ru).all()
+
+
+def test_permute_rejects_bad_ids(ctx):
+    ids = np.array([[1, 2], [3, 9]], np.uint32)     # 9 >= E
+    w = np.ones((2, 2), np.float32)
+    d_ids = torch.from_numpy(ids.astype(np.int32)).cuda()
+    d_w = torch.from_numpy(w).cuda()
+    offs = torch.zeros(9, dtype=torch.int32, device="cuda")
+    ctx.permute(d_ids.data_ptr(), d_w.data_ptr(), 2, 2, 8, offs.data_ptr(), 0, 0, 0, 0)
+    import smoe_amd
+    with pytest.raises(smoe_amd.SmoeError):
+        ctx.synchronize()
+    ctx.synchronize()    # the flag is reported once, then cleared
+
+
+def run_prefill(ctx, layer, T, index0=0, perm=False):
+    h = hidden_states(ctx, T, layer.D, index0=index0)
+    h0 = h.cpu().numpy()
+    ids = torch.zeros((T, layer.K), dtype=torch.int32, device="cuda")
+    w = torch.zeros((T, layer.K), dtype=torch.float32, device="cuda")
+    extra = {}
+    if perm:
+        offs = torch.zeros(layer.E + 1, dtype=torch.int32, device="cuda")
+        tok = torch.zeros(T * layer.K, dtype=torch.int32, device="cuda")
+        uni = torch.zeros(layer.E, dtype=torch.int32, device="cuda")
+        nu = torch.zeros(1, dtype=torch.int32, device="cuda")
+        ctx.moe_prefill(layer.shape, layer.layer, h.data_ptr(), T, ids.data_ptr(), w.data_ptr(),
+                        offs.data_ptr(), tok.data_ptr(), uni.data_ptr(), nu.data_ptr())
+        extra = dict(offs=offs, tok=tok, uni=uni, nu=nu)
+    else:
+        ctx.moe_prefill(layer.shape, layer.layer, h.data_ptr(), T, ids.data_ptr(), w.data_ptr())
+    ctx.synchronize()
+    return h0, h.cpu().numpy(), ids.cpu().numpy().view(np.uint32), w.cpu().numpy(), extra
+
+
+def check_against_oracle(oracle, layer, h0, got, gids, gw, rows=None):
+    rows = np.arange(h0.shape[0]) if rows is None else rows
+    ref, rids, rw = oracle.moe_prefill_layer(layer.oracle_shape(), layer.h_norm, layer.h_router, layer.h_pool,
+                                             layer.stride, layer.off, h0[rows])
+    assert (gids[rows] == rids).all(), np.argwhere(gids[rows] != rids)[:5]
+    assert np.allclose(gw[rows], rw, rtol=1e-5, atol=1e-7)
+    # MoE delta of every token; the residual add is rounded once on each side
+    d_ref = ref.astype(np.float64) - h0[rows]
+    d_got = got[rows].astype(np.float64) - h0[rows]
+    slack = np.spacing(np.abs(got[rows])) + np.spacing(np.abs(ref))
+    worst = 0.0
+    for i in range(len(rows)):
+        e, _ = rel_err(d_got[i], d_ref[i], slack=slack[i])
+        worst = max(worst, e)
+    print(f"prefill rel_err (delta) {worst:.2e} over {len(rows)} tokens")
+    return worst
+
+
+def test_prefill_tiny_shapes(ctx, oracle):
+    for (D, E, K, I, T) in ((128, 16, 4, 128, 70), (256, 64, 8, 192, 33), (512, 200, 6, 256, 9)):
+        layer = Layer(ctx, D, E, K, I, layer_id=100 + D)
+        h0, got, gids, gw, _ = run_prefill(ctx, layer, T)
+        assert check_against_oracle(oracle, layer, h0, got, gids, gw) <= TOL
+
+
+def test_prefill_30b_64_tokens(ctx, oracle):
+    """Qwen3-30B-A3B-shaped layer, one oracle chunk of 64 tokens, with the
+    permute outputs of the same pass checked bit-exactly."""
+    layer = Layer(ctx, 2048, 128, 8, 768, layer_id=3)
+    h0, got, gids, gw, ex = run_prefill(ctx, layer, 64, index0=500, perm=True)
+    assert check_against_oracle(oracle, layer, h0, got, gids, gw) <= TOL
+    ro, rt, _, ru = oracle.permute(gids, gw, 128)
+    assert (ex["offs"].cpu().numpy().view(np.uint32) == ro).all()
+    assert (ex["tok"].cpu().numpy().view(np.uint32) == rt).all()
+    n = int(ex["nu"].item())
+    assert (ex["uni"].cpu().numpy().view(np.uint32)[:n] == ru).all()
+
+
+def test_prefill_30b_512_tokens(ctx, oracle):
+    """Config 4: 512 tokens through one 30B layer.  Every token's ids are
+    checked against the oracle's router + top-k; the hidden update on a sample
+    of 24 tokens spread over the batch (tokens are independent)."""
+    layer = Layer(ctx, 2048, 128, 8, 768, layer_id=4)
+    T = 512
+    h0, got, gids, gw, _ = run_prefill(ctx, layer, T, index0=1000)
+    for t in range(T):
+        x = oracle.rms_norm_bf16(h0[t], layer.h_norm)
+        logits = oracle.matvec_bf16(layer.h_router.reshape(layer.E, layer.D), x)
+        rid, rw = oracle.top_k(logits, layer.K, True)
+        assert (gids[t] == rid).all(), t
+        assert np.allclose(gw[t], rw, rtol=1e-5, atol=1e-7)
+    rows = np.linspace(0, T - 1, 24).astype(int)
+    assert check_against_oracle(oracle, layer, h0, got, gids, gw, rows=rows) <= TOL
+
+
+def test_prefill_235b_shape(ctx, oracle):
+    layer = Layer(ctx, 4096, 128, 8, 1536, layer_id=9)
+    h0, got, gids, gw, _ = run_prefill(ctx, layer, 16, index0=77)
+    assert check_against_oracle(oracle, layer, h0, got, gids, gw) <= TOL
+
+
+def test_prefill_multi_pass_and_no_renorm(ctx, oracle):
+    """More tokens than one permute pass holds (E=512 lowers the limit), and
+    norm_topk off."""
+    layer = Layer(ctx, 256, 512, 8, 128, layer_id=11, norm_topk=False)
+    T = 300
+    h0, got, gids, gw, _ = run_prefill(ctx, layer, T, index0=9)
+    assert check_against_oracle(oracle, layer, h0, got, gids, gw) <= TOL
+
+
+def test_prefill_matches_decode(ctx):
+    """The prefill and decode entry points implement one MoE block: on the same
+    tokens the ids agree and the hidden states agree within the tolerance."""
+    layer = Layer(ctx, 2048, 128, 8, 768, layer_id=5, host=False)
+    T = 8
+    a = hidden_states(ctx, T, 2048, index0=42)
+    x0 = a.cpu().numpy().astype(np.float64)
+    b = a.clone()
+    ia = torch.zeros((T, 8), dtype=torch.int32, device="cuda")
+    ib = torch.zeros_like(ia)
+    ctx.moe_prefill(layer.shape, layer.layer, a.data_ptr(), T, ia.data_ptr())
+    ctx.moe_decode(layer.shape, layer.layer, b.data_ptr(), T, ib.data_ptr())
+    ctx.synchronize()
+    assert (ia.cpu() == ib.cpu()).all()
+    da = a.cpu().numpy() - x0
+    db = b.cpu().numpy() - x0
+    slack = np.spacing(np.abs(a.cpu().numpy())) + np.spacing(np.abs(b.cpu().numpy()))
+    worst = max(rel_err(da[t], db[t], slack=slack[t])[0] for t in range(T))
+    assert worst <= 2 * TOL   # both sides differ from the exact result by up to TOL
