@@ -77,6 +77,11 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="30b", choices=sorted(CONFIGS))
+    ap.add_argument("--workload", default="decode", choices=("decode", "prefill", "batched"),
+                    help="decode: the 48/94-layer batch-1 stack (default); prefill: 512 tokens through one "
+                         "30B layer (configs[3]); batched: 64 tokens through one 235B layer with a Zipf "
+                         "router (configs[4])")
+    ap.add_argument("--replicas", type=int, default=4, help="prefill/batched: layer replicas rotated")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (0: config's)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -99,6 +104,10 @@ def main():
     import torch
 
     import smoe_amd
+
+    if args.workload != "decode":
+        grouped_bench(args)
+        return
 
     c = dict(CONFIGS[args.config])
     if args.layers:
@@ -297,6 +306,141 @@ def cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, targ
         "cpu_seconds": round(total, 3),
         "parity_vs_gpu_step0": {"ids_mismatch": id_mismatch, "max_rel_err_moe_delta": float(f"{worst:.3e}")},
     }
+
+
+# ---------------------------------------------------------------------------
+# prefill and batched decode: the grouped path
+# ---------------------------------------------------------------------------
+GROUPED = {
+    "prefill": dict(D=2048, E=128, K=8, I=768, T=512, zipf=None,
+                    workload="qwen3-30b-a3b-moe-prefill-512"),
+    "batched": dict(D=4096, E=128, K=8, I=1536, T=64, zipf=1.1,
+                    workload="qwen3-235b-a22b-moe-batched-decode-64-zipf1.1"),
+}
+
+
+def zipf_router(torch, ctx, smoe_amd, router, u, D, E, layer, s_exp):
+    """Router rows N(0, 0.02) plus b_e * u with b_e = -s ln(rank_e + 1) / 8
+    (rank = a seeded permutation of the experts), so that hidden states with
+    a fixed component along the unit vector u route with Zipf-like popularity
+    (the reference router has no bias term: this is a generator choice)."""
+    g = torch.Generator().manual_seed(SEED + layer)
+    rank = torch.randperm(E, generator=g).double()
+    b = -s_exp * torch.log(rank + 1.0) / 8.0
+    w = router.view(torch.bfloat16).float().view(E, D).double().cpu()
+    w = w + b[:, None] * u.double().cpu()[None, :]
+    router.copy_(w.float().to(torch.bfloat16).view(torch.int16).view(-1).cuda())
+
+
+def grouped_bench(args):
+    """Tokens/s of the grouped path (smoe_hip_moe_prefill) on one layer shape,
+    rotating over layer replicas (the expert bytes of one replica exceed the
+    256 MB Infinity Cache only partly), each call on the same T seeded hidden
+    rows; per-kernel times from dispatch events."""
+    import torch
+
+    import smoe_amd
+
+    g = GROUPED[args.workload]
+    D, E, K, I, T, R = g["D"], g["E"], g["K"], g["I"], g["T"], args.replicas
+    dev = torch.device("cuda", 0)
+    ctx = smoe_amd.Context()
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    ctx.set_stream(stream.cuda_stream)
+    shape = smoe_amd.make_shape(D, E, K, I)
+    off, raw, stride = smoe_amd.blob_layout(D, I)
+    log(f"{args.workload}: {R} replicas of one layer ({R * E * stride / 1e9:.1f} GB), T={T}")
+    pool = torch.empty(R * E * stride, dtype=torch.uint8, device=dev)
+    ctx.synth_expert_pool(pool.data_ptr(), 0, R, E, stride, shape, SEED, 0.02)
+    router = torch.empty((R, E * D), dtype=torch.int16, device=dev)
+    norm_w = torch.full((D,), 0x3F80, dtype=torch.int16, device=dev)
+    h0 = torch.empty((T, D), dtype=torch.float32, device=dev)
+    for t in range(T):
+        ctx.synth_normal(h0[t].data_ptr(), D, SEED, smoe_amd.hidden_stream(t), 1.0)
+    u = None
+    if g["zipf"]:
+        u = torch.randn(D, generator=torch.Generator().manual_seed(SEED), dtype=torch.float64)
+        u = (u / u.norm()).float().cuda()
+        h0 += 8.0 * u[None, :]          # a fixed component along u (|x . u| ~ 8 of ~64 norm)
+    for l in range(R):
+        ctx.synth_bf16(router[l].data_ptr(), E * D, SEED, smoe_amd.router_stream(l), 0.02)
+        if u is not None:
+            zipf_router(torch, ctx, smoe_amd, router[l], u, D, E, l, g["zipf"])
+    layers = [smoe_amd.make_layer(norm_w.data_ptr(), router[l].data_ptr(), pool.data_ptr() + l * E * stride,
+                                  stride, off) for l in range(R)]
+    hidden = h0.clone()
+    ids = torch.zeros((T, K), dtype=torch.int32, device=dev)
+    ctx.moe_prefill(shape, layers[0], hidden.data_ptr(), T, ids.data_ptr())   # allocates scratch
+    torch.cuda.synchronize()
+
+    def step():
+        for l in range(R):
+            hidden.copy_(h0)
+            ctx.moe_prefill(shape, layers[l], hidden.data_ptr(), T, ids.data_ptr())
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        step()
+    for _ in range(max(1, args.warmup // 4)):
+        graph.replay()
+    torch.cuda.synchronize()
+    steps = max(4, args.steps // 8)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    elapsed = max(time.perf_counter() - t0, ev0.elapsed_time(ev1) / 1e3)
+    calls = steps * R
+    us_per_layer = elapsed * 1e6 / calls
+    ctx.synchronize()
+    counts = torch.bincount(ids.view(-1).long(), minlength=E).cpu()
+    touched = int((counts > 0).sum())
+    # per-kernel times (eager, dispatch events)
+    ctx.profile_enable(True)
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    kern = {}
+    for kid, name in smoe_amd.KERNEL_NAMES.items():
+        n, ms = ctx.profile_read(kid)
+        if n:
+            kern[name] = dict(launches=n, avg_us=round(ms * 1e3 / n, 3))
+    ctx.profile_enable(False)
+    mat = D * I // 2 + D * I // 64 * 2
+    expert_bytes = 3 * mat * touched
+    layer_bytes = expert_bytes + 2 * E * D + T * D * 8
+    pairs = T * K
+    flops = 6 * D * I * pairs + 2 * E * D * T
+    gu, dn = kern.get("grouped_gate_up"), kern.get("grouped_down")
+    gu_bytes, dn_bytes = 2 * mat * touched, mat * touched
+    line = {
+        "metric": f"MoE {args.workload} tok/s & achieved HBM GB/s",
+        "value": round(T * calls / elapsed, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps,
+        "warmup": max(1, args.warmup // 4), "us_per_layer_call": round(us_per_layer, 2),
+        "higher_is_better": True, "dtype": "f32 (f16 hi/lo MFMA)",
+        "data": "synthetic (counter-based N(0,0.02) weights quantized to SMOE-Q4; N(0,1) hidden"
+                + (", router rows biased along a unit vector for Zipf s=1.1 popularity)" if u is not None else ")"),
+        "config": {"workload": g["workload"], "d_model": D, "n_experts": E, "top_k": K, "d_ff": I, "tokens": T,
+                   "replicas": R, "touched_experts": touched, "max_tokens_per_expert": int(counts.max())},
+        "layer_bytes": layer_bytes, "layer_gbs": round(layer_bytes / (us_per_layer * 1e-6) / 1e9, 1),
+        "layer_tflops": round(flops / (us_per_layer * 1e-6) / 1e12, 2),
+        "roofline": {
+            "bound": "hbm", "kernel": "k_grouped_mm<gate_up>",
+            "achieved": round(gu_bytes / (gu["avg_us"] * 1e-6) / 1e9, 1) if gu else None,
+            "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gu_bytes / (gu["avg_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if gu else None,
+            "traffic": None, "bytes_per_launch": gu_bytes,
+            "mfma_tflops_executed": round(2 * 4 * D * I * pairs / (gu["avg_us"] * 1e-6) / 1e12, 1) if gu else None,
+        },
+        "down_gbs": round(dn_bytes / (dn["avg_us"] * 1e-6) / 1e9, 1) if dn else None,
+        "kernels": kern,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
 
 
 # ---------------------------------------------------------------------------

@@ -129,6 +129,51 @@ void smoe_metal_register_buffer(SmoeMetalCtx* ctx, const void* ptr, size_t size_
 /* metal_bridge.h:224 -- number of expert-FFN kernel dispatches submitted. */
 uint64_t smoe_metal_kernel_dispatches(const SmoeMetalCtx* ctx);
 
+/* Dense-trunk symbols that decode.cpp / prefill.cpp also link (outside the MoE
+ * hot path).  metal_bridge.h:157-161 -- output_vec[rows] = weight[rows x cols]
+ * (bf16) . input_vec[cols]; weight is device memory, input_vec / output_vec
+ * are host vectors; synchronous, like the reference. */
+void smoe_metal_scout_matvec_bf16(SmoeMetalCtx* ctx, const uint16_t* weight,
+                                  const float* input_vec, float* output_vec,
+                                  uint32_t rows, uint32_t cols);
+/* metal_bridge.h:198-204 / :210-216 -- count such products, one sync. */
+void smoe_metal_scout_matvec_batch_bf16(SmoeMetalCtx* ctx, const uint16_t** weights,
+                                        const float** inputs, float** outputs,
+                                        const uint32_t* rows, const uint32_t* cols,
+                                        uint32_t count);
+void smoe_metal_scout_matvec_group_bf16(SmoeMetalCtx* ctx, const uint16_t** weights,
+                                        const float** inputs, float** outputs,
+                                        const uint32_t* rows, const uint32_t* cols,
+                                        uint32_t count);
+
+/* metal_bridge.h:166-196 -- fused decode attention.  Attention is outside
+ * this library's scope (the MoE block only): the symbol exists so the
+ * reference callers link; it reports on stderr and leaves o_out untouched. */
+typedef struct {
+    const uint16_t* w_q;
+    const uint16_t* w_k;
+    const uint16_t* w_v;
+    const uint16_t* w_o;
+    const uint16_t* q_norm_w;
+    const uint16_t* k_norm_w;
+    const float*    rope_cos;
+    const float*    rope_sin;
+    const float*    normed_in;
+    float*          qbuf;
+    float*          kbuf;
+    float*          vbuf;
+    float*          k_cache;
+    float*          v_cache;
+    float*          attn_out;
+    float*          o_out;
+    uint32_t d_model, q_dim, kv_dim, head_dim, num_heads, num_kv_heads;
+    uint32_t slot;
+    uint32_t valid;
+    uint32_t attn_ctx;
+    float    attn_scale;
+} SmoeAttnLayerArgs;
+void smoe_metal_attention_layer(SmoeMetalCtx* ctx, const SmoeAttnLayerArgs* args);
+
 /* ======================================================================== */
 /* 2. Device-resident MoE block (MI355X path)                                */
 /* ======================================================================== */

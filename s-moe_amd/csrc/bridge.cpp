@@ -80,6 +80,9 @@ struct SmoeMetalCtx {
     PrefillScratch ps;
     uint32_t* d_err = nullptr;       // [1] device-side error flags (bit 0: exchange time-out, bit 1: bad expert id)
     uint32_t* perm_pairs = nullptr;  // smoe_hip_permute's sorted pair ids
+    float* mv_in = nullptr;          // reference-surface GEMV staging
+    float* mv_out = nullptr;
+    uint32_t mv_cap = 0;
     uint64_t perm_cap = 0;
     std::vector<std::pair<uintptr_t, size_t>> registered;
     char last_err[256] = {0};
@@ -407,6 +410,8 @@ extern "C" void smoe_metal_destroy(SmoeMetalCtx* ctx)
     free_device_scratch(ctx->ds);
     free_prefill_scratch(ctx->ps);
     dfree(ctx->perm_pairs);
+    dfree(ctx->mv_in);
+    dfree(ctx->mv_out);
     dfree(ctx->d_err);
     dfree(ctx->d_input);
     dfree(ctx->d_hidden);
@@ -533,6 +538,61 @@ extern "C" void smoe_metal_register_buffer(SmoeMetalCtx* ctx, const void* ptr, s
         return;
     }
     ctx->registered.emplace_back(p, size_in_bytes);
+}
+
+// dense bf16 GEMVs of the reference surface: host vectors in and out
+static bool matvec_one(SmoeMetalCtx* ctx, const uint16_t* w, const float* in, float* out, uint32_t rows,
+                       uint32_t cols)
+{
+    if (!w || !in || !out || rows == 0 || cols == 0) return false;
+    if (cols > ctx->mv_cap || rows > ctx->mv_cap) {
+        dfree(ctx->mv_in);
+        dfree(ctx->mv_out);
+        ctx->mv_cap = 0;
+        const uint32_t cap = std::max(rows, cols);
+        if (!dalloc(ctx, &ctx->mv_in, cap) || !dalloc(ctx, &ctx->mv_out, cap)) return false;
+        ctx->mv_cap = cap;
+    }
+    return hip_ok(ctx, hipMemcpyAsync(ctx->mv_in, in, size_t(cols) * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+                  "hipMemcpyAsync") &&
+           hip_ok(ctx, smoe::launch_matvec_bf16(w, ctx->mv_in, ctx->mv_out, rows, cols, ctx->stream), "matvec_bf16") &&
+           hip_ok(ctx, hipMemcpyAsync(out, ctx->mv_out, size_t(rows) * sizeof(float), hipMemcpyDeviceToHost,
+                                      ctx->stream),
+                  "hipMemcpyAsync") &&
+           hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+extern "C" void smoe_metal_scout_matvec_bf16(SmoeMetalCtx* ctx, const uint16_t* weight, const float* input_vec,
+                                             float* output_vec, uint32_t rows, uint32_t cols)
+{
+    if (ctx && !matvec_one(ctx, weight, input_vec, output_vec, rows, cols))
+        std::fprintf(stderr, "[smoe_hip] scout_matvec_bf16 failed: %s\n", ctx->last_err);
+}
+
+extern "C" void smoe_metal_scout_matvec_batch_bf16(SmoeMetalCtx* ctx, const uint16_t** weights, const float** inputs,
+                                                   float** outputs, const uint32_t* rows, const uint32_t* cols,
+                                                   uint32_t count)
+{
+    if (!ctx || !weights || !inputs || !outputs || !rows || !cols) return;
+    for (uint32_t i = 0; i < count; ++i)
+        if (!matvec_one(ctx, weights[i], inputs[i], outputs[i], rows[i], cols[i])) {
+            std::fprintf(stderr, "[smoe_hip] scout_matvec_batch_bf16 failed at %u: %s\n", i, ctx->last_err);
+            return;
+        }
+}
+
+extern "C" void smoe_metal_scout_matvec_group_bf16(SmoeMetalCtx* ctx, const uint16_t** weights, const float** inputs,
+                                                   float** outputs, const uint32_t* rows, const uint32_t* cols,
+                                                   uint32_t count)
+{
+    smoe_metal_scout_matvec_batch_bf16(ctx, weights, inputs, outputs, rows, cols, count);
+}
+
+extern "C" void smoe_metal_attention_layer(SmoeMetalCtx* ctx, const SmoeAttnLayerArgs* args)
+{
+    (void)args;
+    if (ctx) std::snprintf(ctx->last_err, sizeof(ctx->last_err), "attention_layer: not provided by this library");
+    std::fprintf(stderr, "[smoe_hip] smoe_metal_attention_layer: attention is outside this library (MoE block only)\n");
 }
 
 extern "C" uint64_t smoe_metal_kernel_dispatches(const SmoeMetalCtx* ctx)

@@ -97,6 +97,10 @@ hipError_t launch_topk(const float* scores, uint32_t rows, uint32_t n, uint32_t 
                        uint32_t norm, uint32_t* ids, float* w, hipStream_t s);
 
 
+// out [rows] = W [rows x cols] bf16 . x [cols] (reference-surface dense GEMV)
+hipError_t launch_matvec_bf16(const uint16_t* W, const float* x, float* out, uint32_t rows, uint32_t cols,
+                              hipStream_t s);
+
 // ---- prefill, T token rows (moe_prefill.hip) -----------------------------
 // RMSNorm + router + top-k for T tokens: normed [T x D], ids/w [T x K].
 hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, float* normed,

@@ -590,4 +590,31 @@ hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const fl
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// k_matvec_bf16: out[r] = sum_c bf16(W[r][c]) * x[c] (common.hpp:293-306), one
+// wave per row, any cols (the dense-trunk projections of the reference
+// surface, metal_bridge.h:157-161; not on the MoE hot path).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256)
+void k_matvec_bf16(const uint16_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ out,
+                   uint32_t rows, uint32_t cols)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const uint16_t* wr = W + static_cast<size_t>(r) * cols;
+    float acc = 0.f;
+    for (uint32_t c = lane; c < cols; c += WAVE) acc = fmaf(bf16_to_f32(wr[c]), x[c], acc);
+    acc = wave_sum(acc);
+    if (lane == 0) out[r] = acc;
+}
+
+hipError_t launch_matvec_bf16(const uint16_t* W, const float* x, float* out, uint32_t rows, uint32_t cols,
+                              hipStream_t s)
+{
+    if (rows == 0 || cols == 0) return hipErrorInvalidValue;
+    launch_kernel(k_matvec_bf16, dim3((rows + 3) / 4), dim3(256), s, W, x, out, rows, cols);
+    return hipGetLastError();
+}
+
 }  // namespace smoe

@@ -74,6 +74,10 @@ SIGNATURES = [
     ("smoe_metal_wait_ffn_batch", None, [_VP, _VP, _VP, _U32, _U32]),
     ("smoe_metal_register_buffer", None, [_VP, _VP, _SZ]),
     ("smoe_metal_kernel_dispatches", _U64, [_VP]),
+    ("smoe_metal_scout_matvec_bf16", None, [_VP, _VP, _VP, _VP, _U32, _U32]),
+    ("smoe_metal_scout_matvec_batch_bf16", None, [_VP, _VP, _VP, _VP, _VP, _VP, _U32]),
+    ("smoe_metal_scout_matvec_group_bf16", None, [_VP, _VP, _VP, _VP, _VP, _VP, _U32]),
+    ("smoe_metal_attention_layer", None, [_VP, _VP]),
     ("smoe_hip_set_stream", _I, [_VP, _VP]),
     ("smoe_hip_synchronize", _I, [_VP]),
     ("smoe_hip_reserve", _I, [_VP, _SHP, _U32]),
@@ -92,8 +96,10 @@ SIGNATURES = [
 
 KERNEL_MOE_UP, KERNEL_GATE_UP, KERNEL_MOE_DOWN, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
 KERNEL_PERMUTE, KERNEL_GROUPED_GATE_UP, KERNEL_GROUPED_DOWN, KERNEL_SCATTER = 5, 6, 7, 8
+KERNEL_ROUTE, KERNEL_SPLIT = 9, 10
 KERNEL_NAMES = {0: "moe_up", 1: "gate_up", 2: "moe_down", 3: "down_slots", 4: "topk",
-                5: "permute", 6: "grouped_gate_up", 7: "grouped_down", 8: "scatter"}
+                5: "permute", 6: "grouped_gate_up", 7: "grouped_down", 8: "combine", 9: "route",
+                10: "split"}
 
 _lib = None
 

@@ -84,3 +84,32 @@ def test_reference_surface_rejections(ctx):
     assert L.smoe_hip_moe_decode(ctx.ptr, C.byref(shape), C.byref(lay), 1 << 20, 1, None, None) == smoe_amd.SMOE_ERR_SHAPE
     shape = smoe_amd.make_shape(2000, 128, 8, 768)
     assert L.smoe_hip_moe_decode(ctx.ptr, C.byref(shape), C.byref(lay), 1 << 20, 1, None, None) == smoe_amd.SMOE_ERR_SHAPE
+
+
+def test_scout_matvec_bf16(ctx, oracle):
+    """metal_bridge.h:157-161: dense bf16 GEMV with host vectors, and the
+    batch form (metal_bridge.h:198-204), against the compiled-reference-pinned
+    oracle matvec (rtol 1e-5: only the fp32 summation order differs)."""
+    L = smoe_amd.lib()
+    rng = np.random.default_rng(3)
+    for rows, cols in ((128, 2048), (37, 100), (512, 4096)):
+        w = torch.empty(rows * cols, dtype=torch.int16, device="cuda")
+        ctx.synth_bf16(w.data_ptr(), rows * cols, 5, rows, 0.02)
+        x = rng.standard_normal(cols).astype(np.float32)
+        out = np.zeros(rows, np.float32)
+        L.smoe_metal_scout_matvec_bf16(ctx.ptr, w.data_ptr(), x.ctypes.data, out.ctypes.data, rows, cols)
+        ref = oracle.matvec_bf16(w.cpu().numpy().view(np.uint16).reshape(rows, cols), x)
+        assert np.allclose(out, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+    # batch of two
+    ws = [torch.empty(64 * 256, dtype=torch.int16, device="cuda") for _ in range(2)]
+    for i, w in enumerate(ws):
+        ctx.synth_bf16(w.data_ptr(), 64 * 256, 6, i, 0.02)
+    xs = [rng.standard_normal(256).astype(np.float32) for _ in range(2)]
+    outs = [np.zeros(64, np.float32) for _ in range(2)]
+    VP = C.c_void_p
+    L.smoe_metal_scout_matvec_batch_bf16(
+        ctx.ptr, (VP * 2)(*[w.data_ptr() for w in ws]), (VP * 2)(*[x.ctypes.data for x in xs]),
+        (VP * 2)(*[o.ctypes.data for o in outs]), (C.c_uint32 * 2)(64, 64), (C.c_uint32 * 2)(256, 256), 2)
+    for w, x, o in zip(ws, xs, outs):
+        ref = oracle.matvec_bf16(w.cpu().numpy().view(np.uint16).reshape(64, 256), x)
+        assert np.allclose(o, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
