@@ -42,7 +42,7 @@ struct PrefillScratch {
     float* normed = nullptr;        // [T x D]
     uint16_t* x_hi = nullptr;       // [T x D] f16
     uint16_t* x_lo = nullptr;
-    float2* x_st = nullptr;         // [T x D/64]
+    float* x_sc = nullptr;          // [T] row scales
     uint32_t* ids = nullptr;        // [T x K]
     float* w = nullptr;             // [T x K]
     uint32_t* offsets = nullptr;    // [E + 1]
@@ -50,7 +50,7 @@ struct PrefillScratch {
     float* h = nullptr;             // [P x I]
     uint16_t* h_hi = nullptr;       // [P x I] f16
     uint16_t* h_lo = nullptr;
-    float2* h_st = nullptr;         // [P x I/64]
+    float* h_sc = nullptr;          // [P] row scales
     float* y = nullptr;             // [P x D]
 };
 
@@ -141,7 +141,7 @@ void free_prefill_scratch(PrefillScratch& s)
     dfree(s.normed);
     dfree(s.x_hi);
     dfree(s.x_lo);
-    dfree(s.x_st);
+    dfree(s.x_sc);
     dfree(s.ids);
     dfree(s.w);
     dfree(s.offsets);
@@ -149,7 +149,7 @@ void free_prefill_scratch(PrefillScratch& s)
     dfree(s.h);
     dfree(s.h_hi);
     dfree(s.h_lo);
-    dfree(s.h_st);
+    dfree(s.h_sc);
     dfree(s.y);
     s = PrefillScratch{};
 }
@@ -268,10 +268,10 @@ int ensure_prefill_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
     free_prefill_scratch(c);
     const size_t T_ = n.T, P = T_ * n.K;
     const bool ok = dalloc(ctx, &n.normed, T_ * n.D) && dalloc(ctx, &n.x_hi, T_ * n.D) &&
-                    dalloc(ctx, &n.x_lo, T_ * n.D) && dalloc(ctx, &n.x_st, T_ * n.D / 64) &&
+                    dalloc(ctx, &n.x_lo, T_ * n.D) && dalloc(ctx, &n.x_sc, T_) &&
                     dalloc(ctx, &n.ids, P) && dalloc(ctx, &n.w, P) && dalloc(ctx, &n.offsets, size_t(n.E) + 1) &&
                     dalloc(ctx, &n.pairs, P) && dalloc(ctx, &n.h, P * n.I) && dalloc(ctx, &n.h_hi, P * n.I) &&
-                    dalloc(ctx, &n.h_lo, P * n.I) && dalloc(ctx, &n.h_st, P * n.I / 64) && dalloc(ctx, &n.y, P * n.D);
+                    dalloc(ctx, &n.h_lo, P * n.I) && dalloc(ctx, &n.h_sc, P) && dalloc(ctx, &n.y, P * n.D);
     if (!ok) {
         free_prefill_scratch(n);
         return SMOE_ERR_HIP;
@@ -699,18 +699,18 @@ extern "C" int smoe_hip_moe_prefill(SmoeMetalCtx* ctx, const SmoeMoeShape* shape
         if (!timed(ctx, SMOE_KERNEL_ROUTE, "route",
                    [&] { return smoe::launch_route(d, L, hv, T, s.normed, ids, w, st); }) ||
             !timed(ctx, SMOE_KERNEL_SPLIT, "split(x)",
-                   [&] { return smoe::launch_split_rows(s.normed, T, d.D, s.x_hi, s.x_lo, s.x_st, st); }) ||
+                   [&] { return smoe::launch_split_rows(s.normed, T, d.D, s.x_hi, s.x_lo, s.x_sc, st); }) ||
             !timed(ctx, SMOE_KERNEL_PERMUTE, "permute", [&] {
                 return smoe::launch_permute(ids, w, P, d.K, d.E, offs, s.pairs, sorted_tokens, nullptr, union_ids,
                                             union_size, ctx->d_err, st);
             }) ||
             !timed(ctx, SMOE_KERNEL_GROUPED_GATE_UP, "grouped_gate_up", [&] {
-                return smoe::launch_grouped_gate_up(d, L, offs, s.pairs, s.x_hi, s.x_lo, s.x_st, s.h, st);
+                return smoe::launch_grouped_gate_up(d, L, offs, s.pairs, s.x_hi, s.x_lo, s.x_sc, s.h, st);
             }) ||
             !timed(ctx, SMOE_KERNEL_SPLIT, "split(h)",
-                   [&] { return smoe::launch_split_rows(s.h, P, d.I, s.h_hi, s.h_lo, s.h_st, st); }) ||
+                   [&] { return smoe::launch_split_rows(s.h, P, d.I, s.h_hi, s.h_lo, s.h_sc, st); }) ||
             !timed(ctx, SMOE_KERNEL_GROUPED_DOWN, "grouped_down", [&] {
-                return smoe::launch_grouped_down(d, L, offs, s.pairs, s.h_hi, s.h_lo, s.h_st, s.y, st);
+                return smoe::launch_grouped_down(d, L, offs, s.pairs, s.h_hi, s.h_lo, s.h_sc, s.y, st);
             }) ||
             !timed(ctx, SMOE_KERNEL_SCATTER, "combine",
                    [&] { return smoe::launch_combine_pairs(s.y, w, T, d.K, d.D, hv, st); }))

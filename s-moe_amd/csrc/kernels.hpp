@@ -105,10 +105,10 @@ hipError_t launch_matvec_bf16(const uint16_t* W, const float* x, float* out, uin
 // RMSNorm + router + top-k for T tokens: normed [T x D], ids/w [T x K].
 hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, float* normed,
                         uint32_t* ids, float* w, hipStream_t s);
-// Per (row, 64-column group) of src [rows x cols]: f16 hi/lo planes of
-// x * 2^-e (|x| < 2^e) and st = (sum of hi + lo, 2^e).
+// Per row of src [rows x cols]: f16 hi/lo planes of x * 2^-e (|x| < 2^e over
+// the row) and scale[row] = 2^e.
 hipError_t launch_split_rows(const float* src, uint32_t rows, uint32_t cols, uint16_t* hi, uint16_t* lo,
-                             float2* st, hipStream_t s);
+                             float* scale, hipStream_t s);
 // Stable counting sort of the P pairs by expert: offsets [E+1],
 // sorted_pairs [P] (pair = token * K + rank); sorted_tokens, sorted_w,
 // union_ids [E], union_size [1] optional (nullptr).  Bad ids set err bit 1.
@@ -121,10 +121,10 @@ hipError_t launch_permute(const uint32_t* ids, const float* w, uint32_t P, uint3
 // h [P x I] = silu(x G^T) * (x U^T); y [P x D] = h Dn^T.
 hipError_t launch_grouped_gate_up(const MoeDims& d, const LayerDesc& L, const uint32_t* offsets,
                                   const uint32_t* sorted_pairs, const uint16_t* x_hi, const uint16_t* x_lo,
-                                  const float2* x_st, float* h, hipStream_t s);
+                                  const float* x_scale, float* h, hipStream_t s);
 hipError_t launch_grouped_down(const MoeDims& d, const LayerDesc& L, const uint32_t* offsets,
                                const uint32_t* sorted_pairs, const uint16_t* h_hi, const uint16_t* h_lo,
-                               const float2* h_st, float* y, hipStream_t s);
+                               const float* h_scale, float* y, hipStream_t s);
 // hidden[t] += sum_r w[t][r] * y[t*K + r] (rank order).
 hipError_t launch_combine_pairs(const float* y, const float* w, uint32_t T, uint32_t K, uint32_t D, float* hidden,
                                 hipStream_t s);

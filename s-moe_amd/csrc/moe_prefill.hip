@@ -10,23 +10,24 @@
 //
 //   k_route        RMSNorm + fp32 router + exact top-k for TB tokens per
 //                  block; writes the normed rows (fp32) and ids/weights.
-//   k_split_rows   per (row, 64-column group): power-of-two scale 2^e with
-//                  |x| < 2^e, f16 hi/lo planes of x * 2^-e (hi + lo carries
-//                  22 bits), and the group sum of hi + lo.
+//   k_split_rows   per row: power-of-two scale 2^e with |x| < 2^e and the
+//                  f16 hi/lo planes of x * 2^-e (hi + lo carries 22 bits).
 //   k_permute      stable counting sort of the T*k (token, rank) pairs by
 //                  expert (one workgroup), union order by first appearance.
 //   k_grouped_mm   per expert: [tokens x K] x [K x 64 rows] tiles on MFMA
-//                  v_mfma_f32_16x16x32_f16.  Weights enter exactly as c - 8
-//                  (f16), activations as hi and lo planes (two MFMAs into one
-//                  fp32 accumulator), each 64-column group closes with the
-//                  dequant epilogue s_g * 2^e * (acc + 0.5 * sum) / 7.5
-//                  (kernels.metal:140-145).  Gate+up runs with SiLU and writes
-//                  h per (token, rank) pair; down writes y per pair.
+//                  v_mfma_f32_16x16x32_f16, activation chunks staged in LDS.
+//                  Weights enter exactly as 2c - 15 (f16), activations as hi
+//                  and lo planes (two MFMAs into one fp32 accumulator); each
+//                  64-column group adds s_g * sum, the row scale 2^e / 15
+//                  closes the dot (kernels.metal:90-105, 140-145).  Gate+up
+//                  runs with SiLU and writes h per (token, rank) pair; down
+//                  writes y per pair.
 //   k_combine_pairs hidden[t] += sum_r w[t][r] * y[t*k + r] in rank order.
 //
 // Blocks of one expert are mapped to one XCD (block id mod 8), so its token
 // rows stay in that XCD's L2 while the expert's weights stream once.
 #include <algorithm>
+#include <type_traits>
 
 #include "device_common.hpp"
 #include "kernels.hpp"
@@ -37,6 +38,7 @@ namespace smoe {
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
 // k_route: RMSNorm (common.hpp:245-256) + router (common.hpp:293-306) +
@@ -169,29 +171,41 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
 }
 
 // ---------------------------------------------------------------------------
-// k_split_rows: src [rows x cols] fp32 -> f16 planes hi/lo of x * 2^-e per
-// (row, 64-column group) with |x| < 2^e, and st[row][group] = (sum of
-// hi + lo over the group, 2^e).  One wave per (row, group).
+// k_split_rows: src [rows x cols] fp32 -> f16 planes hi/lo of x * 2^-e with
+// |x| < 2^e over the row, and scale[row] = 2^e.  hi + lo carries 22 bits of
+// x * 2^-e (f16 subnormals below 2^-14 still hold x to 2^-25 of the row max).
+// One wave per row.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256)
 void k_split_rows(const float* __restrict__ src, uint32_t rows, uint32_t cols, uint16_t* __restrict__ hi,
-                  uint16_t* __restrict__ lo, float2* __restrict__ st)
+                  uint16_t* __restrict__ lo, float* __restrict__ scale)
 {
     const int lane = threadIdx.x & 63;
-    const uint32_t G = cols >> 6, total = rows * G;
-    for (uint32_t it = blockIdx.x * 4 + (threadIdx.x >> 6); it < total; it += gridDim.x * 4) {
-        const uint32_t r = it / G, g = it - r * G;
-        const size_t o = static_cast<size_t>(r) * cols + g * 64 + lane;
-        const float x = src[o];
-        const float amax = wave_max(fabsf(x));
+    for (uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6); r < rows; r += gridDim.x * 4) {
+        const float* x = src + static_cast<size_t>(r) * cols;
+        float amax = 0.f;
+        for (uint32_t c = lane * 4; c < cols; c += WAVE * 4) {
+            const float4 v = load_f4(x + c);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+        amax = wave_max(amax);
         const int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
-        const float xs = __builtin_ldexpf(x, -e);
-        const _Float16 h = static_cast<_Float16>(xs);
-        const _Float16 l = static_cast<_Float16>(xs - static_cast<float>(h));
-        hi[o] = __builtin_bit_cast(uint16_t, h);
-        lo[o] = __builtin_bit_cast(uint16_t, l);
-        const float sum = wave_sum(static_cast<float>(h) + static_cast<float>(l));
-        if (lane == 0) st[it] = make_float2(sum, __builtin_ldexpf(1.0f, e));
+        for (uint32_t c = lane * 4; c < cols; c += WAVE * 4) {
+            const float4 v = load_f4(x + c);
+            const float xs[4] = {__builtin_ldexpf(v.x, -e), __builtin_ldexpf(v.y, -e), __builtin_ldexpf(v.z, -e),
+                                 __builtin_ldexpf(v.w, -e)};
+            uint16_t h4[4], l4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const _Float16 h = static_cast<_Float16>(xs[i]);
+                h4[i] = __builtin_bit_cast(uint16_t, h);
+                l4[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(xs[i] - static_cast<float>(h)));
+            }
+            const size_t o = static_cast<size_t>(r) * cols + c;
+            *reinterpret_cast<uint2*>(hi + o) = make_uint2(h4[0] | (uint32_t(h4[1]) << 16), h4[2] | (uint32_t(h4[3]) << 16));
+            *reinterpret_cast<uint2*>(lo + o) = make_uint2(l4[0] | (uint32_t(l4[1]) << 16), l4[2] | (uint32_t(l4[3]) << 16));
+        }
+        if (lane == 0) scale[r] = __builtin_ldexpf(1.0f, e);
     }
 }
 
@@ -296,20 +310,32 @@ void k_permute(const uint32_t* __restrict__ ids, const float* __restrict__ w, ui
 
 // ---------------------------------------------------------------------------
 // k_grouped_mm: for each expert e with M = offsets[e+1] - offsets[e] pairs,
-// out[pair][n] over a 64-row tile of its weight matrix (gate+up or down).
-// Block = 4 waves, wave w owns rows n0 + 16 w .. + 16; a pass covers 32
-// pairs as two 16-row MFMA tiles.  v_mfma_f32_16x16x32_f16 operand layout:
-// lane l holds A[l % 16][8 (l / 16) + j] and B[8 (l / 16) + j][l % 16]
-// (j < 8) and receives D[4 (l / 16) + i][l % 16] (i < 4).  Inside a 64-column
-// group, lane quarter q = l / 16 of MFMA step s uses physical columns
-// 16 q + 8 s + j, so each lane reads 8 contiguous bytes of packed weights and
-// 32 contiguous bytes of each activation plane per group.
+// out[pair][n] for a 64-row tile of its weight matrix (gate+up or down).
+// Block = 4 waves; wave w owns rows n0 + 16 w .. + 16 (one MFMA tile); a pass
+// covers 64 pairs as four 16-row tiles (one pass for up to 64 pairs, so each
+// weight is read and converted once per expert).  The k dimension runs in
+// chunks of 128 columns: the block stages the chunk's activation rows (f16 hi
+// and lo planes) in LDS once for its 4 waves, and the next chunk's weights and
+// activation rows are loaded into registers while the current chunk computes.
+//
+// v_mfma_f32_16x16x32_f16 operand layout: lane l holds A[l % 16][8 (l/16) + j]
+// and B[8 (l/16) + j][l % 16] (j < 8) and receives D[4 (l/16) + i][l % 16].
+// Inside a 64-column group, lane quarter q = l/16 of MFMA step s uses the
+// physical columns 16 q + 8 s + j, so each lane reads 8 contiguous bytes of
+// packed weights per group.  Weights enter as f16 (2c - 15) (exact), so a
+// group's MFMA sum times s_g is 15/7.5 of its dequantised dot product
+// (kernels.metal:90-105, 140-145) and the epilogue is one FMA per output.
 // ---------------------------------------------------------------------------
 constexpr int MM_WAVES = 4;
-constexpr int MM_ROWS = 16 * MM_WAVES;   // weight rows per block
-constexpr int MM_PASS = 32;              // pairs per pass
+constexpr int MM_NS = 1;                          // 16-row weight tiles per wave
+constexpr int MM_ROWS = 16 * MM_NS * MM_WAVES;    // weight rows per block
+constexpr int MM_MS = 4;                          // 16-pair tiles per pass
+constexpr int MM_PASS = 16 * MM_MS;               // pairs per pass
+constexpr int MM_KC = 128;                        // columns per chunk (2 groups)
+constexpr int MM_GC = MM_KC / 64;
+constexpr int MM_LDS_ROW = MM_KC + 8;             // f16 per staged row (+16 B: spreads LDS banks)
 
-// eight codes (one dword, low nibble first) -> f16 (c - 8), exact.
+// eight codes (one dword, low nibble first) -> f16 (2c - 15), exact.
 // The bias is added to the whole half8 at once: assembling the half8 element
 // by element from four half2 sums was miscompiled by this toolchain (hipcc
 // 7.2, gfx950: the four pairs collapsed into copies of the first).
@@ -317,45 +343,46 @@ __device__ __forceinline__ half8_t q4_codes_to_f16(uint32_t v)
 {
     const uint32_t E = v & 0x0F0F0F0Fu;          // codes 0, 2, 4, 6
     const uint32_t O = (v >> 4) & 0x0F0F0F0Fu;   // codes 1, 3, 5, 7
-    // f16 bits 0x6400 | c = 1024 + c exactly; minus 1032 -> c - 8 exactly
+    // f16 bits 0x6400 | 2c = 1024 + 2c exactly; minus 1039 -> 2c - 15 exactly
     u32x4_t r;
-    r.x = __builtin_amdgcn_perm(O, E, 0x0C040C00u) | 0x64006400u;
-    r.y = __builtin_amdgcn_perm(O, E, 0x0C050C01u) | 0x64006400u;
-    r.z = __builtin_amdgcn_perm(O, E, 0x0C060C02u) | 0x64006400u;
-    r.w = __builtin_amdgcn_perm(O, E, 0x0C070C03u) | 0x64006400u;
-    const _Float16 b = static_cast<_Float16>(-1032.0f);
+    r.x = (__builtin_amdgcn_perm(O, E, 0x0C040C00u) << 1) | 0x64006400u;
+    r.y = (__builtin_amdgcn_perm(O, E, 0x0C050C01u) << 1) | 0x64006400u;
+    r.z = (__builtin_amdgcn_perm(O, E, 0x0C060C02u) << 1) | 0x64006400u;
+    r.w = (__builtin_amdgcn_perm(O, E, 0x0C070C03u) << 1) | 0x64006400u;
+    const _Float16 b = static_cast<_Float16>(-1039.0f);
     const half8_t bias = {b, b, b, b, b, b, b, b};
     return __builtin_bit_cast(half8_t, r) + bias;
 }
 
-__device__ __forceinline__ half8_t load_half8(const uint16_t* p)
+__device__ __forceinline__ half8_t lds_half8(const uint16_t* p)
 {
-    const uint4 v = load_u4(p);
+    const uint4 v = *reinterpret_cast<const uint4*>(__builtin_assume_aligned(p, 16));
     u32x4_t u;
     u.x = v.x; u.y = v.y; u.z = v.z; u.w = v.w;
     return __builtin_bit_cast(half8_t, u);
 }
 
-template <bool GATE_UP>
-__global__ __launch_bounds__(MM_WAVES * WAVE)
-void k_grouped_mm(MoeDims d, LayerDesc L, const uint32_t* __restrict__ offsets,
-                  const uint32_t* __restrict__ sorted_pairs, const uint16_t* __restrict__ a_hi,
-                  const uint16_t* __restrict__ a_lo, const float2* __restrict__ a_st, uint32_t a_row_div,
-                  float* __restrict__ out, uint32_t n_dim, uint32_t k_dim, uint32_t n_tiles)
+template <bool GATE_UP, int MS>
+__device__ __forceinline__ void grouped_mm_expert(
+    const MoeDims& d, const LayerDesc& L, uint32_t e, uint32_t tile, uint32_t base, uint32_t M,
+    const uint32_t* __restrict__ sorted_pairs, const uint16_t* __restrict__ a_hi, const uint16_t* __restrict__ a_lo,
+    const float* __restrict__ a_scale, uint32_t a_row_div, float* __restrict__ out, uint32_t n_dim, uint32_t k_dim,
+    uint16_t (&s_a)[2][MM_PASS][MM_LDS_ROW], uint32_t (&s_row)[MM_PASS], uint32_t (&s_pair)[MM_PASS])
 {
     constexpr int NM = GATE_UP ? 2 : 1;
-    __shared__ uint32_t s_row[MM_PASS];    // activation row of pass pair m
-    __shared__ uint32_t s_pair[MM_PASS];
+    constexpr int PASS = 16 * MS;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const uint32_t b = blockIdx.x, xcd = b & 7u, j = b >> 3;
-    const uint32_t e = xcd + 8u * (j / n_tiles), tile = j % n_tiles;
-    if (e >= d.E) return;
-    const uint32_t base = offsets[e], M = offsets[e + 1] - base;
-    if (M == 0) return;
 
     const uint32_t G = k_dim >> 6;
-    const uint32_t n = tile * MM_ROWS + wv * 16 + (lane & 15);
     const uint32_t q = lane >> 4;
+    uint32_t n[MM_NS];
+    bool n_ok[MM_NS];
+#pragma unroll
+    for (int ns = 0; ns < MM_NS; ++ns) {
+        const uint32_t r = tile * MM_ROWS + wv * (16 * MM_NS) + ns * 16 + (lane & 15);
+        n_ok[ns] = r < n_dim;
+        n[ns] = min(r, n_dim - 1);
+    }
     const uint8_t* blob = L.experts + static_cast<size_t>(e) * L.stride;
     const uint8_t* wp[NM];
     const uint16_t* sp[NM];
@@ -369,97 +396,169 @@ void k_grouped_mm(MoeDims d, LayerDesc L, const uint32_t* __restrict__ offsets,
         sp[0] = reinterpret_cast<const uint16_t*>(blob + L.off[5]);
     }
     const size_t row_bytes = k_dim >> 1;
+    // staging role of this thread: rows tm and tm + 32, 32 columns at ts * 32
+    // of each chunk (4 threads per row and chunk)
+    const uint32_t tm = threadIdx.x >> 2, ts = threadIdx.x & 3;
+    const uint32_t nck = (k_dim + MM_KC - 1) / MM_KC;
 
-    for (uint32_t m0 = 0; m0 < M; m0 += MM_PASS) {
+    for (uint32_t m0 = 0; m0 < M; m0 += PASS) {
         __syncthreads();
-        if (threadIdx.x < MM_PASS) {
+        if (threadIdx.x < PASS) {
             const uint32_t p = sorted_pairs[base + min(m0 + threadIdx.x, M - 1)];
             s_pair[threadIdx.x] = p;
             s_row[threadIdx.x] = p / a_row_div;
         }
         __syncthreads();
-        // A-operand rows of this lane (row l % 16 of each 16-pair tile)
-        const uint16_t* ah[2];
-        const uint16_t* al[2];
-#pragma unroll
-        for (int ms = 0; ms < 2; ++ms) {
-            const size_t r = s_row[16 * ms + (lane & 15)];
-            ah[ms] = a_hi + r * k_dim + 16 * q;
-            al[ms] = a_lo + r * k_dim + 16 * q;
-        }
-        // epilogue rows of this lane: D rows 4 q + i of each tile
-        uint32_t er[2][4];
-#pragma unroll
-        for (int ms = 0; ms < 2; ++ms)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) er[ms][i] = s_row[16 * ms + 4 * q + i];
+        const size_t arow = static_cast<size_t>(s_row[min(tm, static_cast<uint32_t>(PASS - 1))]) * k_dim;
 
-        f32x4_t acc[2][NM];
+        // chunk loaders: weights (per wave) and this thread's activation share
+        uint2 wq[2][MM_NS][NM][MM_GC];
+        uint16_t sq[2][MM_NS][NM][MM_GC];
+        uint4 ah[4], al[4];
+        auto load_chunk = [&](uint32_t c, int buf_rt) {
+            const int buf = buf_rt;
+            const uint32_t kc = c * MM_KC;
+            const uint32_t gc = min(static_cast<uint32_t>(MM_KC), k_dim - kc) >> 6;
 #pragma unroll
-        for (int ms = 0; ms < 2; ++ms)
+            for (int ns = 0; ns < MM_NS; ++ns)
 #pragma unroll
-            for (int mt = 0; mt < NM; ++mt) acc[ms][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-        for (uint32_t g = 0; g < G; ++g) {
-            uint2 wq[NM];
-            float sc[NM];
+                for (int mt = 0; mt < NM; ++mt)
 #pragma unroll
-            for (int mt = 0; mt < NM; ++mt) {
-                const uint8_t* wr = wp[mt] + n * row_bytes + g * 32 + 8 * q;
-                wq[mt].x = __builtin_nontemporal_load(gptr(reinterpret_cast<const uint32_t*>(wr)));
-                wq[mt].y = __builtin_nontemporal_load(gptr(reinterpret_cast<const uint32_t*>(wr) + 1));
-                sc[mt] = f16_bits_to_f32(load_stream_u16(sp[mt] + static_cast<size_t>(n) * G + g));
+                    for (int g = 0; g < MM_GC; ++g) {
+                        const uint32_t gg = min(static_cast<uint32_t>(g), gc - 1);
+                        const u32x2_t* wr = reinterpret_cast<const u32x2_t*>(
+                            wp[mt] + n[ns] * row_bytes + (kc >> 1) + gg * 32 + 8 * q);
+                        const u32x2_t w2 = __builtin_nontemporal_load(gptr(wr));
+                        wq[buf][ns][mt][g] = make_uint2(w2.x, w2.y);
+                        sq[buf][ns][mt][g] =
+                            load_stream_u16(sp[mt] + static_cast<size_t>(n[ns]) * G + (kc >> 6) + gg);
+                    }
+            const uint32_t col = kc + min(ts * 32, gc * 64 - 32);
+            if (tm >= static_cast<uint32_t>(PASS)) return;   // rows past this pass width stay unused
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                ah[2 * i] = load_u4(a_hi + arow + col + 16 * i);
+                ah[2 * i + 1] = load_u4(a_hi + arow + col + 16 * i + 8);
+                al[2 * i] = load_u4(a_lo + arow + col + 16 * i);
+                al[2 * i + 1] = load_u4(a_lo + arow + col + 16 * i + 8);
             }
-            half8_t xa[2][2][2];   // [ms][step][hi/lo]
+        };
+
+        f32x4_t acc[MS][MM_NS][NM];
 #pragma unroll
-            for (int ms = 0; ms < 2; ++ms) {
+        for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-                for (int s = 0; s < 2; ++s) {
-                    xa[ms][s][0] = load_half8(ah[ms] + g * 64 + 8 * s);
-                    xa[ms][s][1] = load_half8(al[ms] + g * 64 + 8 * s);
+            for (int ns = 0; ns < MM_NS; ++ns)
+#pragma unroll
+                for (int mt = 0; mt < NM; ++mt) acc[ms][ns][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+        // one chunk: stage its activations, start the next chunk's loads, compute
+        auto step = [&](uint32_t c, auto cur_tag) {
+            constexpr int CUR = decltype(cur_tag)::value;
+            const uint32_t gc = min(static_cast<uint32_t>(MM_KC), k_dim - c * MM_KC) >> 6;
+            __syncthreads();                     // the previous chunk's readers are done
+            if (ts * 32 < gc * 64 && tm < static_cast<uint32_t>(PASS)) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    *reinterpret_cast<uint4*>(&s_a[0][tm][ts * 32 + 8 * i]) = ah[i];
+                    *reinterpret_cast<uint4*>(&s_a[1][tm][ts * 32 + 8 * i]) = al[i];
                 }
             }
-            float2 st[2][4];
+            __syncthreads();
+            if (c + 1 < nck) load_chunk(c + 1, CUR ^ 1);   // in flight while this chunk computes
 #pragma unroll
-            for (int ms = 0; ms < 2; ++ms)
+            for (int g = 0; g < MM_GC; ++g) {
+                if (static_cast<uint32_t>(g) >= gc) break;
+                half8_t b[MM_NS][NM][2];
+                float sc[MM_NS][NM];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) st[ms][i] = a_st[static_cast<size_t>(er[ms][i]) * G + g];
+                for (int ns = 0; ns < MM_NS; ++ns)
 #pragma unroll
-            for (int mt = 0; mt < NM; ++mt) {
-                const half8_t b0 = q4_codes_to_f16(wq[mt].x);
-                const half8_t b1 = q4_codes_to_f16(wq[mt].y);
+                    for (int mt = 0; mt < NM; ++mt) {
+                        b[ns][mt][0] = q4_codes_to_f16(wq[CUR][ns][mt][g].x);
+                        b[ns][mt][1] = q4_codes_to_f16(wq[CUR][ns][mt][g].y);
+                        sc[ns][mt] = f16_bits_to_f32(sq[CUR][ns][mt][g]);
+                    }
 #pragma unroll
-                for (int ms = 0; ms < 2; ++ms) {
-                    f32x4_t t = {0.f, 0.f, 0.f, 0.f};
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[ms][0][0], b0, t, 0, 0, 0);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[ms][0][1], b0, t, 0, 0, 0);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[ms][1][0], b1, t, 0, 0, 0);
-                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[ms][1][1], b1, t, 0, 0, 0);
+                for (int ms = 0; ms < MS; ++ms) {
+                    half8_t xa[2][2];   // [step][hi/lo]
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc[ms][mt][i] = fmaf(sc[mt] * st[ms][i].y, fmaf(0.5f, st[ms][i].x, t[i]), acc[ms][mt][i]);
+                    for (int st = 0; st < 2; ++st)
+#pragma unroll
+                        for (int pl = 0; pl < 2; ++pl)
+                            xa[st][pl] = lds_half8(&s_a[pl][16 * ms + (lane & 15)][g * 64 + 16 * q + 8 * st]);
+#pragma unroll
+                    for (int ns = 0; ns < MM_NS; ++ns)
+#pragma unroll
+                        for (int mt = 0; mt < NM; ++mt) {
+                            f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+                            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[0][0], b[ns][mt][0], t, 0, 0, 0);
+                            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[0][1], b[ns][mt][0], t, 0, 0, 0);
+                            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1][0], b[ns][mt][1], t, 0, 0, 0);
+                            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1][1], b[ns][mt][1], t, 0, 0, 0);
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                acc[ms][ns][mt][i] = fmaf(sc[ns][mt], t[i], acc[ms][ns][mt][i]);
+                        }
                 }
             }
+        };
+        load_chunk(0, 0);
+        for (uint32_t c = 0; c < nck; c += 2) {
+            step(c, std::integral_constant<int, 0>{});
+            if (c + 1 < nck) step(c + 1, std::integral_constant<int, 1>{});
         }
-        // outputs: pair rows 4 q + i of each tile, column n
+        // outputs: pair rows 4 q + i of each tile, columns n; value = acc * 2^e_row / 15
 #pragma unroll
-        for (int ms = 0; ms < 2; ++ms) {
+        for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t m = 16 * ms + 4 * q + i;
                 if (m0 + m >= M) continue;
-                float* o = out + static_cast<size_t>(s_pair[m]) * n_dim + n;
-                const float v0 = acc[ms][0][i] * (1.0f / 7.5f);
-                if (GATE_UP) {
-                    const float v1 = acc[ms][NM - 1][i] * (1.0f / 7.5f);
-                    // h = silu(g) * u, silu(z) = z * (1 / (1 + exp(-z)))  (kernels.metal:61-63)
-                    *o = (v0 * (1.0f / (1.0f + expf(-v0)))) * v1;
-                } else {
-                    *o = v0;
+                const float rs = a_scale[s_row[m]] * (1.0f / 15.0f);
+                float* o = out + static_cast<size_t>(s_pair[m]) * n_dim;
+#pragma unroll
+                for (int ns = 0; ns < MM_NS; ++ns) {
+                    if (!n_ok[ns]) continue;
+                    const float v0 = acc[ms][ns][0][i] * rs;
+                    if (GATE_UP) {
+                        const float v1 = acc[ms][ns][NM - 1][i] * rs;
+                        // h = silu(g) * u, silu(z) = z * (1 / (1 + exp(-z)))  (kernels.metal:61-63)
+                        o[n[ns]] = (v0 * (1.0f / (1.0f + expf(-v0)))) * v1;
+                    } else {
+                        o[n[ns]] = v0;
+                    }
                 }
             }
         }
     }
+}
+
+template <bool GATE_UP>
+__global__ __launch_bounds__(MM_WAVES * WAVE, 2)
+void k_grouped_mm(MoeDims d, LayerDesc L, const uint32_t* __restrict__ offsets,
+                  const uint32_t* __restrict__ sorted_pairs, const uint16_t* __restrict__ a_hi,
+                  const uint16_t* __restrict__ a_lo, const float* __restrict__ a_scale, uint32_t a_row_div,
+                  float* __restrict__ out, uint32_t n_dim, uint32_t k_dim, uint32_t n_tiles)
+{
+    __shared__ __align__(16) uint16_t s_a[2][MM_PASS][MM_LDS_ROW];
+    __shared__ uint32_t s_row[MM_PASS];
+    __shared__ uint32_t s_pair[MM_PASS];
+    const uint32_t b = blockIdx.x, xcd = b & 7u, jb = b >> 3;
+    const uint32_t e = xcd + 8u * (jb / n_tiles), tile = jb % n_tiles;
+    if (e >= d.E) return;
+    const uint32_t base = offsets[e], M = offsets[e + 1] - base;
+    if (M == 0) return;
+    // pass width by the expert's pair count: MFMA rows past M are wasted work
+    if (M <= 16)
+        grouped_mm_expert<GATE_UP, 1>(d, L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, a_row_div, out,
+                                      n_dim, k_dim, s_a, s_row, s_pair);
+    else if (M <= 32)
+        grouped_mm_expert<GATE_UP, 2>(d, L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, a_row_div, out,
+                                      n_dim, k_dim, s_a, s_row, s_pair);
+    else
+        grouped_mm_expert<GATE_UP, MM_MS>(d, L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, a_row_div, out,
+                                          n_dim, k_dim, s_a, s_row, s_pair);
 }
 
 // ---------------------------------------------------------------------------
@@ -508,12 +607,11 @@ hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidde
 }
 
 hipError_t launch_split_rows(const float* src, uint32_t rows, uint32_t cols, uint16_t* hi, uint16_t* lo,
-                             float2* st, hipStream_t s)
+                             float* scale, hipStream_t s)
 {
     if (cols % 64 || rows == 0) return hipErrorInvalidValue;
-    const uint32_t items = rows * (cols / 64);
-    const uint32_t blocks = std::min<uint32_t>((items + 3) / 4, 8192u);
-    launch_kernel(k_split_rows, dim3(blocks), dim3(256), s, src, rows, cols, hi, lo, st);
+    const uint32_t blocks = std::min<uint32_t>((rows + 3) / 4, 8192u);
+    launch_kernel(k_split_rows, dim3(blocks), dim3(256), s, src, rows, cols, hi, lo, scale);
     return hipGetLastError();
 }
 
@@ -536,23 +634,23 @@ hipError_t launch_permute(const uint32_t* ids, const float* w, uint32_t P, uint3
 
 hipError_t launch_grouped_gate_up(const MoeDims& d, const LayerDesc& L, const uint32_t* offsets,
                                   const uint32_t* sorted_pairs, const uint16_t* x_hi, const uint16_t* x_lo,
-                                  const float2* x_st, float* h, hipStream_t s)
+                                  const float* x_scale, float* h, hipStream_t s)
 {
-    if (d.group != 64 || d.I % MM_ROWS || d.D % 64) return hipErrorInvalidValue;
-    const uint32_t n_tiles = d.I / MM_ROWS, eg = (d.E + 7) / 8;
+    if (d.group != 64 || d.I % 64 || d.D % 64) return hipErrorInvalidValue;
+    const uint32_t n_tiles = (d.I + MM_ROWS - 1) / MM_ROWS, eg = (d.E + 7) / 8;
     launch_kernel(k_grouped_mm<true>, dim3(8 * eg * n_tiles), dim3(MM_WAVES * WAVE), s, d, L, offsets, sorted_pairs,
-                  x_hi, x_lo, x_st, d.K, h, d.I, d.D, n_tiles);
+                  x_hi, x_lo, x_scale, d.K, h, d.I, d.D, n_tiles);
     return hipGetLastError();
 }
 
 hipError_t launch_grouped_down(const MoeDims& d, const LayerDesc& L, const uint32_t* offsets,
                                const uint32_t* sorted_pairs, const uint16_t* h_hi, const uint16_t* h_lo,
-                               const float2* h_st, float* y, hipStream_t s)
+                               const float* h_scale, float* y, hipStream_t s)
 {
-    if (d.group != 64 || d.D % MM_ROWS || d.I % 64) return hipErrorInvalidValue;
-    const uint32_t n_tiles = d.D / MM_ROWS, eg = (d.E + 7) / 8;
+    if (d.group != 64 || d.D % 64 || d.I % 64) return hipErrorInvalidValue;
+    const uint32_t n_tiles = (d.D + MM_ROWS - 1) / MM_ROWS, eg = (d.E + 7) / 8;
     launch_kernel(k_grouped_mm<false>, dim3(8 * eg * n_tiles), dim3(MM_WAVES * WAVE), s, d, L, offsets,
-                  sorted_pairs, h_hi, h_lo, h_st, 1u, y, d.D, d.I, n_tiles);
+                  sorted_pairs, h_hi, h_lo, h_scale, 1u, y, d.D, d.I, n_tiles);
     return hipGetLastError();
 }
 
