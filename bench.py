@@ -38,7 +38,7 @@ CONFIGS = {
 }
 HBM_PEAK_GBS = 8000.0
 SEED = 20261201
-KERNEL_SYMBOLS = {"moe_up": "k_moe_up", "moe_down": "k_down_combine"}
+KERNEL_SYMBOLS = {"moe_up": "k_moe_up", "moe_down": "k_down_combine", "decode_stack": "k_decode_stack"}
 
 
 def log(msg):
@@ -46,10 +46,14 @@ def log(msg):
 
 
 def kernel_bytes(c):
-    """Algorithmic HBM bytes per launch of each decode kernel (one token-layer)."""
+    """Algorithmic HBM bytes per launch of each decode kernel: one token-layer
+    for the two-launch path; one token through every layer for the stack
+    kernel (per layer k * B_expert + 2 E D router + 12 D for x, hidden in and
+    hidden out)."""
     D, E, K, I = c["D"], c["E"], c["K"], c["I"]
     mat = D * I // 2 + D * I // 64 * 2            # packed nibbles + fp16 scales of one matrix
     return {
+        "decode_stack": c["layers"] * (K * 3 * mat + 2 * E * D + 12 * D),
         # router bf16 + norm weights + hidden in + 8 experts' gate+up + h out
         "moe_up": E * D * 2 + D * 2 + D * 4 + K * 2 * mat + K * I * 4,
         # 8 experts' down + h in + weights + hidden read and written
@@ -84,6 +88,9 @@ def main():
     ap.add_argument("--replicas", type=int, default=4, help="prefill/batched: layer replicas rotated")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (0: config's)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
+    ap.add_argument("--engine", default="layers", choices=("stack", "layers"),
+                    help="stack: the whole step in one persistent launch (smoe_hip_moe_decode_stack); "
+                         "layers: two launches per layer (smoe_hip_moe_decode)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU work the baseline sample aims at")
     ap.add_argument("--profile-steps", type=int, default=8, help="replays of the event-timed step (0: skip)")
@@ -148,10 +155,17 @@ def main():
                                   stride, off) for l in range(NL)]
     ctx.reserve(shape, 1)
     torch.cuda.synchronize()
+    layer_arr = (smoe_amd.SmoeMoeLayer * NL)(*layers)
 
-    def step():
-        for l in range(NL):
-            ctx.moe_decode(shape, layers[l], hidden.data_ptr(), 1)
+    if args.engine == "stack":
+        def step():
+            ctx.moe_decode_stack(shape, layer_arr, hidden.data_ptr())
+    else:
+        def step():
+            for l in range(NL):
+                ctx.moe_decode(shape, layers[l], hidden.data_ptr(), 1)
+    step()                      # scratch and layer table, outside capture
+    torch.cuda.synchronize()
 
     graph = None
     if not args.no_graph:
@@ -194,6 +208,7 @@ def main():
         "config": {"workload": c["workload"], "d_model": D, "n_experts": E, "top_k": K, "d_ff": I,
                    "layers": NL, "batch": 1, "decode_steps": args.steps,
                    "quant": "SMOE-Q4 g64 fp16 absmax", "launch": "hip-graph" if graph else "eager",
+                   "engine": "persistent stack kernel" if args.engine == "stack" else "two launches per layer",
                    "resident_expert_bytes": NL * E * raw},
     }
 
@@ -212,13 +227,14 @@ def main():
             "timing": how,
         }
         line["kernels"] = kern
-        layer_bytes = sum(kb.values())
+        layer_bytes = kb["decode_stack"] // NL
         line["layer_bytes"] = layer_bytes
+        # whole-step algorithmic bytes over the timed step time (launch gaps included)
         line["stack_gbs"] = round(layer_bytes * NL * tok_s / 1e9, 1)
 
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off,
-                                            args.cpu_seconds)
+                                            args.cpu_seconds, args.engine)
     print(json.dumps(line), flush=True)
     ctx.close()
 
@@ -240,14 +256,15 @@ def kernel_times(ctx, torch, stream, step, replays):
 
 def _read_profile(ctx, smoe_amd):
     out = {}
-    for kid, name in ((smoe_amd.KERNEL_MOE_UP, "moe_up"), (smoe_amd.KERNEL_MOE_DOWN, "moe_down")):
+    for kid, name in ((smoe_amd.KERNEL_MOE_UP, "moe_up"), (smoe_amd.KERNEL_MOE_DOWN, "moe_down"),
+                      (smoe_amd.KERNEL_STACK, "decode_stack")):
         n, ms = ctx.profile_read(kid)
         if n:
             out[name] = (n, ms * 1e3 / n)
     return out
 
 
-def cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, target_s):
+def cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, target_s, engine="stack"):
     """The CPU oracle (fp32 restatement, one thread) on whole decode steps of
     the same stack, repeated until about `target_s` seconds of CPU work (at
     least one step, at most 3 x target); host copies of the weights are made
@@ -281,7 +298,10 @@ def cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, targ
                 gpu_h.copy_(torch.from_numpy(h))
                 lay = smoe_amd.make_layer(norm_w.data_ptr(), router[l].data_ptr(),
                                           pool.data_ptr() + l * layer_bytes, stride, off)
-                ctx.moe_decode(shape, lay, gpu_h.data_ptr(), 1, ids.data_ptr())
+                if engine == "stack":
+                    ctx.moe_decode_stack(shape, [lay], gpu_h.data_ptr(), ids.data_ptr())
+                else:
+                    ctx.moe_decode(shape, lay, gpu_h.data_ptr(), 1, ids.data_ptr())
                 torch.cuda.synchronize()
             t0 = time.perf_counter()
             out, oid, ow, _lg, _nr, yo = O.moe_decode_layer(oshape, h_norm, h_routers[l], h_pools[l], stride,

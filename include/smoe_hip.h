@@ -231,6 +231,22 @@ int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
                         const SmoeMoeLayer* layer, float* hidden, uint32_t n_tokens,
                         uint32_t* ids_out, float* weights_out);
 
+/* One batch-1 decode step through a stack of MoE layers: the layer loop of
+ * decode.cpp:121 over the block above, hidden [d_model] (device, in place)
+ *   for l in 0 .. n_layers-1:  hidden += MoE_l(RMSNorm_l(hidden))
+ * with layers [n_layers] a host array of layer descriptors (all of one shape).
+ * The whole step is one persistent kernel launch (no per-layer kernel
+ * boundary); results equal n_layers calls of smoe_hip_moe_decode up to fp32
+ * summation order.  ids_out / weights_out [n_layers x top_k] are optional
+ * device outputs (rank order, renormalised, decode.cpp:285-307).  The layer
+ * table is copied to the device when it differs from the previous call's
+ * (outside graph capture; under capture a new table gives SMOE_ERR_CAPTURE).
+ * Shapes the persistent kernel does not cover (d_model > 4096, d_ff > 2048,
+ * more than 512 experts) run as n_layers smoe_hip_moe_decode calls. */
+int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
+                              const SmoeMoeLayer* layers, uint32_t n_layers, float* hidden,
+                              uint32_t* ids_out, float* weights_out);
+
 /* Prefill MoE block (prefill.cpp:308-453) over n_tokens rows [n_tokens x
  * d_model]: per token RMSNorm + router + top-k, then the layer-major expert
  * grouping (token-by-expert permute, grouped expert GEMMs on MFMA, weighted
@@ -305,6 +321,7 @@ int smoe_hip_synth_expert_pool(SmoeMetalCtx* ctx, uint8_t* base, uint32_t first_
 #define SMOE_KERNEL_SCATTER       8   /* prefill: weighted combine of pair outputs + residual */
 #define SMOE_KERNEL_ROUTE         9   /* prefill: RMSNorm + router + top-k per token          */
 #define SMOE_KERNEL_SPLIT        10   /* prefill: f16 hi/lo planes of activations             */
+#define SMOE_KERNEL_STACK        11   /* decode: every layer of a stack in one launch         */
 #define SMOE_KERNEL_KINDS        16
 int smoe_hip_profile_enable(SmoeMetalCtx* ctx, int enable);
 int smoe_hip_profile_read(SmoeMetalCtx* ctx, uint32_t kernel, uint64_t* launches, double* total_ms);

@@ -54,6 +54,16 @@ struct PrefillScratch {
     float* y = nullptr;             // [P x D]
 };
 
+// persistent stack kernel: exchange words, control words, device layer table
+struct StackScratch {
+    size_t words = 0;               // capacity of xch
+    uint64_t* xch = nullptr;        // exchange words (zeroed once; the kernel keeps them)
+    uint32_t* ctl = nullptr;        // [ST_CTL_WORDS] control words (likewise)
+    LayerDesc* tbl = nullptr;       // [tbl_cap] device copy of the layer table
+    uint32_t tbl_cap = 0;
+    std::vector<LayerDesc> host_tbl;   // what tbl holds
+};
+
 }  // namespace
 
 struct SmoeMetalCtx {
@@ -78,6 +88,7 @@ struct SmoeMetalCtx {
 
     DeviceScratch ds;
     PrefillScratch ps;
+    StackScratch ss;
     uint32_t* d_err = nullptr;       // [1] device-side error flags (bit 0: exchange time-out, bit 1: bad expert id)
     uint32_t* perm_pairs = nullptr;  // smoe_hip_permute's sorted pair ids
     float* mv_in = nullptr;          // reference-surface GEMV staging
@@ -409,6 +420,9 @@ extern "C" void smoe_metal_destroy(SmoeMetalCtx* ctx)
     if (ctx->own_stream && ctx->own_stream != ctx->stream) (void)hipStreamSynchronize(ctx->own_stream);
     free_device_scratch(ctx->ds);
     free_prefill_scratch(ctx->ps);
+    dfree(ctx->ss.xch);
+    dfree(ctx->ss.ctl);
+    dfree(ctx->ss.tbl);
     dfree(ctx->perm_pairs);
     dfree(ctx->mv_in);
     dfree(ctx->mv_out);
@@ -622,9 +636,12 @@ extern "C" int smoe_hip_synchronize(SmoeMetalCtx* ctx)
         if (e) {
             // reported once: clear for the next call
             if (!hip_ok(ctx, hipMemset(ctx->d_err, 0, sizeof(uint32_t)), "hipMemset(err)")) return SMOE_ERR_HIP;
-            std::snprintf(ctx->last_err, sizeof(ctx->last_err), "device:%s%s (flags %u)",
-                          (e & 1u) ? " routing exchange timed out" : "", (e & 2u) ? " expert id out of range" : "", e);
-            return (e & 1u) ? SMOE_ERR_HIP : SMOE_ERR_ARG;
+            std::snprintf(ctx->last_err, sizeof(ctx->last_err), "device:%s%s%s (flags %u)",
+                          (e & 1u) ? " routing exchange timed out" : "", (e & 2u) ? " expert id out of range" : "",
+                          (e & 4u) ? " a stack block ran off its XCD (later calls write exchange words through)"
+                                   : "",
+                          e);
+            return (e & 5u) ? SMOE_ERR_HIP : SMOE_ERR_ARG;
         }
     }
     return SMOE_OK;
@@ -667,6 +684,85 @@ extern "C" int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
                                    float* hidden, uint32_t n_tokens, uint32_t* ids_out, float* weights_out)
 {
     return moe_forward(ctx, shape, layer, hidden, n_tokens, ids_out, weights_out);
+}
+
+static bool same_layer(const LayerDesc& a, const LayerDesc& b)
+{
+    return std::memcmp(&a, &b, sizeof(LayerDesc)) == 0;
+}
+
+extern "C" int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, const SmoeMoeLayer* layers,
+                                         uint32_t n_layers, float* hidden, uint32_t* ids_out, float* weights_out)
+{
+    if (!ctx || !shape || !layers || !hidden || n_layers == 0) return SMOE_ERR_ARG;
+    for (uint32_t l = 0; l < n_layers; ++l)
+        if (!layers[l].norm_w || !layers[l].router_w || !layers[l].experts) return SMOE_ERR_ARG;
+    int rc = shape_check(shape);
+    if (rc != SMOE_OK) return rc;
+    const MoeDims d = dims_of(shape);
+    if (!smoe::stack_supported(d)) {
+        // outside the persistent kernel's shapes: one decode call per layer
+        for (uint32_t l = 0; l < n_layers; ++l) {
+            rc = moe_forward(ctx, shape, &layers[l], hidden, 1, ids_out ? ids_out + size_t(l) * d.K : nullptr,
+                             weights_out ? weights_out + size_t(l) * d.K : nullptr);
+            if (rc != SMOE_OK) return rc;
+        }
+        return SMOE_OK;
+    }
+    StackScratch& s = ctx->ss;
+    const bool capturing = stream_capturing(ctx->stream);
+    // exchange words: grown (and zeroed) outside capture only
+    const size_t words = smoe::stack_xch_words(d, std::min<uint32_t>(n_layers, smoe::ST_MAX_LAYERS));
+    if (!s.ctl || s.words < words) {
+        if (capturing) return SMOE_ERR_CAPTURE;
+        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
+        dfree(s.xch);
+        s.words = 0;
+        if (!s.ctl) {
+            if (!dalloc(ctx, &s.ctl, smoe::ST_CTL_WORDS) ||
+                !hip_ok(ctx, hipMemset(s.ctl, 0, smoe::ST_CTL_WORDS * sizeof(uint32_t)), "hipMemset(ctl)"))
+                return SMOE_ERR_HIP;
+        }
+        // flags only ever grow (the control word keeps the epoch), so fresh
+        // zeroed words can never match a live flag
+        if (!dalloc(ctx, &s.xch, words) ||
+            !hip_ok(ctx, hipMemset(s.xch, 0, words * sizeof(uint64_t)), "hipMemset(xch)"))
+            return SMOE_ERR_HIP;
+        s.words = words;
+    }
+    // device layer table: uploaded when it changes (outside capture)
+    bool same = s.tbl && s.host_tbl.size() == n_layers;
+    for (uint32_t l = 0; same && l < n_layers; ++l) same = same_layer(s.host_tbl[l], layer_of(&layers[l]));
+    if (!same) {
+        if (capturing) return SMOE_ERR_CAPTURE;
+        std::vector<LayerDesc> t(n_layers);
+        for (uint32_t l = 0; l < n_layers; ++l) t[l] = layer_of(&layers[l]);
+        // the previous table may still be read by queued work
+        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
+        if (s.tbl_cap < n_layers) {
+            dfree(s.tbl);
+            s.tbl_cap = 0;
+            if (!dalloc(ctx, &s.tbl, n_layers)) return SMOE_ERR_HIP;
+            s.tbl_cap = n_layers;
+        }
+        if (!hip_ok(ctx, hipMemcpy(s.tbl, t.data(), n_layers * sizeof(LayerDesc), hipMemcpyHostToDevice),
+                    "hipMemcpy(layer table)"))
+            return SMOE_ERR_HIP;
+        s.host_tbl = std::move(t);
+    }
+    // one launch per ST_MAX_LAYERS layers (the kernel keeps its layer table in LDS)
+    for (uint32_t l0 = 0; l0 < n_layers; l0 += smoe::ST_MAX_LAYERS) {
+        const uint32_t n = std::min<uint32_t>(smoe::ST_MAX_LAYERS, n_layers - l0);
+        if (!timed(ctx, SMOE_KERNEL_STACK, "decode_stack", [&] {
+                return smoe::launch_decode_stack(d, s.tbl + l0, n, hidden, s.xch, s.ctl,
+                                                 ids_out ? ids_out + size_t(l0) * d.K : nullptr,
+                                                 weights_out ? weights_out + size_t(l0) * d.K : nullptr,
+                                                 ctx->d_err, ctx->stream);
+            }))
+            return SMOE_ERR_HIP;
+    }
+    ctx->dispatches.fetch_add(uint64_t(n_layers) * d.K, std::memory_order_relaxed);
+    return SMOE_OK;
 }
 
 extern "C" int smoe_hip_moe_prefill(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, const SmoeMoeLayer* layer,

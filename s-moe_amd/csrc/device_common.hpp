@@ -188,6 +188,58 @@ __device__ __forceinline__ float wave_sum_rows(const float (&v)[N])
     return a[0];
 }
 
+// ---- segmented transposed reduction ---------------------------------------
+// Sums N per-lane values over segments of 2^SEG lanes (the lanes sharing
+// l >> SEG), N a power of two with log2 N <= SEG <= 6.  The butterfly runs
+// over lane bits SEG-1 .. 0 with the cross-lane steps of wave_sum_rows; the
+// first log2 N steps split the values (lanes with the bit clear keep the
+// lower half of the indices), the rest are plain sums.  Lane l returns the
+// segment total of value (l >> (SEG - log2 N)) & (N - 1).
+template <int BIT, bool SPLIT>
+__device__ __forceinline__ void red_bit(float& lo, float hi, int lane)
+{
+    if constexpr (BIT == 5) {
+        swap32_sum(lo, SPLIT ? hi : lo);
+    } else if constexpr (BIT == 4) {
+        swap16_sum(lo, SPLIT ? hi : lo);
+    } else {
+        constexpr int CTRL = BIT == 3 ? DPP_ROW_ROR8
+                           : BIT == 2 ? DPP_ROW_HALF_MIRROR
+                           : BIT == 1 ? DPP_QUAD_XOR2
+                                      : DPP_QUAD_XOR1;
+        if constexpr (SPLIT)
+            dpp_split_sum<CTRL>(lo, hi, lane & (1 << BIT));
+        else
+            lo += dpp_f32<CTRL>(0.f, lo);
+    }
+}
+
+template <int SEG, int M, int N>
+__device__ __forceinline__ void seg_steps(float (&a)[N], int lane)
+{
+    if constexpr (SEG > 0) {
+        if constexpr (M > 1) {
+#pragma unroll
+            for (int i = 0; i < M / 2; ++i) red_bit<SEG - 1, true>(a[i], a[i + M / 2], lane);
+            seg_steps<SEG - 1, M / 2>(a, lane);
+        } else {
+            red_bit<SEG - 1, false>(a[0], a[0], lane);
+            seg_steps<SEG - 1, 1>(a, lane);
+        }
+    }
+}
+
+template <int N, int SEG>
+__device__ __forceinline__ float seg_sum_rows(const float (&v)[N])
+{
+    static_assert((N & (N - 1)) == 0 && ilog2(N) <= SEG && SEG <= 6, "N must be a power of two <= 2^SEG");
+    float a[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) a[i] = v[i];
+    seg_steps<SEG, N>(a, threadIdx.x & 63);
+    return a[0];
+}
+
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 {
     v = max(v, dpp_u32<DPP_QUAD_XOR1>(0u, v));

@@ -97,6 +97,23 @@ hipError_t launch_topk(const float* scores, uint32_t rows, uint32_t n, uint32_t 
                        uint32_t norm, uint32_t* ids, float* w, hipStream_t s);
 
 
+// ---- decode, whole stack in one persistent launch (moe_stack.hip) ---------
+// 256 blocks of 4 waves, one per CU of MI355X (8 XCDs x 32 CUs).
+constexpr int ST_BLOCKS = 256;
+constexpr int ST_WPB = 4;
+constexpr int ST_THREADS = ST_WPB * 64;
+constexpr uint32_t ST_WX = ST_BLOCKS / 8 * ST_WPB;   // waves per XCD
+constexpr uint32_t ST_CTL_WORDS = 352;               // control words (11 lines of 128 B)
+constexpr uint32_t ST_MAX_LAYERS = 128;              // layers per launch (the table sits in LDS)
+bool stack_supported(const MoeDims& d);
+// exchange words (uint64) the stack kernel needs for n_layers layers
+size_t stack_xch_words(const MoeDims& d, uint32_t n_layers);
+// hidden [D] += MoE_l(RMSNorm(hidden)) for l = 0 .. n_layers-1 (layers: device
+// array, n_layers <= ST_MAX_LAYERS); ids/w [n_layers x K] optional.  xch zeroed once at allocation, ctl
+// [ST_CTL_WORDS] likewise; both are kept by the kernel between calls.
+hipError_t launch_decode_stack(const MoeDims& d, const LayerDesc* layers, uint32_t n_layers, float* hidden,
+                               uint64_t* xch, uint32_t* ctl, uint32_t* ids, float* w, uint32_t* err, hipStream_t s);
+
 // out [rows] = W [rows x cols] bf16 . x [cols] (reference-surface dense GEMV)
 hipError_t launch_matvec_bf16(const uint16_t* W, const float* x, float* out, uint32_t rows, uint32_t cols,
                               hipStream_t s);

@@ -56,6 +56,7 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
 {
     constexpr int RPB = 16 / TB;   // router rows per reduction batch (RPB * TB values)
     __shared__ float s_logit[TB][SMOE_TOPK_MAX_N];
+    __shared__ uint2 s_slots[TB][TOPK_SLOTS];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint32_t t0 = blockIdx.x * TB;
     const uint32_t D = d.D, nch = D >> 5;
@@ -162,7 +163,7 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
         }
         uint32_t my_id;
         float my_w;
-        const uint32_t count = topk_fast<VPL>(p, d.E, d.K, d.norm_topk, my_id, my_w);
+        const uint32_t count = topk_fast<VPL>(p, d.E, d.K, d.norm_topk, my_id, my_w, s_slots[wv]);
         if (static_cast<uint32_t>(lane) < count) {
             ids[static_cast<size_t>(t0 + wv) * d.K + lane] = my_id;
             w[static_cast<size_t>(t0 + wv) * d.K + lane] = my_w;

@@ -97,19 +97,25 @@ __device__ void topk_select(float (&p)[VPL], uint32_t (&id)[VPL], uint32_t (&key
 
 // ---------------------------------------------------------------------------
 // Softmax + top-k of n scores held in one wave (position p = lane + 64 j).
-// Fast path: count rounds of max extraction.  Round s takes the wave maximum
-// of the remaining keys; when exactly one position holds it, that position is
-// what the reference's round s of selection with swaps (scout.cpp:101-110)
-// picks, whatever the earlier swaps moved, since a strict maximum wins the
-// strict '>' scan from any arrangement.  A maximum held by two positions (a
-// tie, where positions and swaps decide) or any NaN sends the row to the
-// exact swap emulation topk_select.  A unique maximum in the last round also
-// proves it strictly above every unselected key.
+// Fast path: count rounds of max extraction, all in the vector unit.  Round
+// s takes the wave maximum K of the remaining keys and marks every position
+// holding K with rank s (removing it).  When every round removes exactly one
+// position, that position is what the reference's round s of selection with
+// swaps (scout.cpp:101-110) picks, whatever the earlier swaps moved, since a
+// strict maximum wins the strict '>' scan from any arrangement; a unique
+// maximum in the last round is also strictly above every unselected key.  So
+// the fast result stands when the rounds removed exactly count positions; a
+// tie (two positions removed in one round) or any NaN sends the row to the
+// exact swap emulation topk_select.  The ranked (position, probability) pairs
+// are gathered through `slots` (16 entries of LDS private to this wave) and
+// the renormalisation sum runs in rank order, as the reference's.
 // Lane r < count receives (id_r, w_r); returns count.
 // ---------------------------------------------------------------------------
+constexpr uint32_t TOPK_SLOTS = 16;   // LDS uint2 entries per wave (k <= 16)
+
 template <int VPL>
 __device__ uint32_t topk_fast(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t norm, uint32_t& my_id,
-                              float& my_w)
+                              float& my_w, uint2* slots)
 {
     const int lane = threadIdx.x & (WAVE - 1);
     // softmax (scout.cpp:85-98)
@@ -127,52 +133,51 @@ __device__ uint32_t topk_fast(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t 
     }
     sum = wave_sum(sum);
     const float inv_sum = (sum > 0.f) ? 1.0f / sum : 0.f;
-    uint32_t key[VPL], id[VPL];
+    uint32_t key[VPL], rem[VPL], rank[VPL];
     bool nan = false;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const uint32_t pos = lane + WAVE * j;
         v[j] *= inv_sum;
-        id[j] = pos;
         nan |= pos < n && isnan(v[j]);
         key[j] = pos < n ? (isnan(v[j]) ? 1u : __float_as_uint(v[j]) + 1u) : 0u;
+        rem[j] = key[j];
+        rank[j] = TOPK_SLOTS;
     }
     const uint32_t count = k < n ? k : n;
     if (__ballot(nan) == 0) {
-        uint32_t rem[VPL];
-#pragma unroll
-        for (int j = 0; j < VPL; ++j) rem[j] = key[j];
-        uint32_t rid = 0;
-        float rw = 0.f, ksum = 0.f;
-        bool unique = true;
-        for (uint32_t s = 0; s < count && unique; ++s) {
+        for (uint32_t s = 0; s < count; ++s) {
             uint32_t lk = rem[0];
 #pragma unroll
             for (int j = 1; j < VPL; ++j) lk = max(lk, rem[j]);
-            const uint32_t kmax = wave_max_u32(lk);
-            uint32_t hits = 0, pos = 0;
+            const uint32_t K = wave_max_u32(lk);
 #pragma unroll
-            for (int j = VPL - 1; j >= 0; --j) {
-                const uint64_t b = __ballot(rem[j] == kmax);
-                hits += __popcll(b);
-                if (b != 0) pos = WAVE * j + __builtin_ctzll(b);
-                if (rem[j] == kmax) rem[j] = 0u;
-            }
-            unique = hits == 1;
-            const float ps = readlane_f32(sel(v, pos >> 6), pos & 63);
-            ksum += ps;                                 // rank order, as the reference
-            if (static_cast<uint32_t>(lane) == s) {
-                rid = pos;
-                rw = ps;
+            for (int j = 0; j < VPL; ++j) {
+                const bool hit = rem[j] == K;
+                rank[j] = hit ? s : rank[j];
+                rem[j] = hit ? 0u : rem[j];
             }
         }
-        if (unique) {
-            my_id = rid;
-            my_w = rw;
-            if (norm && ksum > 0.f) my_w = my_w * (1.0f / ksum);
+        uint32_t removed = 0;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) removed += __popcll(__ballot(rank[j] < TOPK_SLOTS));
+        if (removed == count) {
+#pragma unroll
+            for (int j = 0; j < VPL; ++j)
+                if (rank[j] < TOPK_SLOTS) slots[rank[j]] = make_uint2(lane + WAVE * j, __float_as_uint(v[j]));
+            // the wave's LDS writes complete in order before its read
+            const uint2 e = slots[min(static_cast<uint32_t>(lane), TOPK_SLOTS - 1)];
+            float ksum = 0.f;
+            for (uint32_t r = 0; r < count; ++r) ksum += __uint_as_float(readlane_u32(e.y, static_cast<int>(r)));
+            my_id = static_cast<uint32_t>(lane) < count ? e.x : 0u;
+            my_w = static_cast<uint32_t>(lane) < count ? __uint_as_float(e.y) : 0.f;
+            if (norm && ksum > 0.f) my_w = my_w * (1.0f / ksum);   // rank order, as the reference
             return count;
         }
     }
+    uint32_t id[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) id[j] = lane + WAVE * j;
     topk_select<VPL>(v, id, key, count, norm, my_id, my_w);
     return count;
 }

@@ -82,6 +82,7 @@ SIGNATURES = [
     ("smoe_hip_synchronize", _I, [_VP]),
     ("smoe_hip_reserve", _I, [_VP, _SHP, _U32]),
     ("smoe_hip_moe_decode", _I, [_VP, _SHP, _LAY, _VP, _U32, _VP, _VP]),
+    ("smoe_hip_moe_decode_stack", _I, [_VP, _SHP, _LAY, _U32, _VP, _VP, _VP]),
     ("smoe_hip_moe_prefill", _I, [_VP, _SHP, _LAY, _VP, _U32, _VP, _VP, _VP, _VP, _VP, _VP]),
     ("smoe_hip_compute_top_k", _I, [_VP, _VP, _U32, _U32, _U32, _VP, _VP, _I]),
     ("smoe_hip_permute", _I, [_VP, _VP, _VP, _U32, _U32, _U32, _VP, _VP, _VP, _VP, _VP]),
@@ -96,10 +97,10 @@ SIGNATURES = [
 
 KERNEL_MOE_UP, KERNEL_GATE_UP, KERNEL_MOE_DOWN, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
 KERNEL_PERMUTE, KERNEL_GROUPED_GATE_UP, KERNEL_GROUPED_DOWN, KERNEL_SCATTER = 5, 6, 7, 8
-KERNEL_ROUTE, KERNEL_SPLIT = 9, 10
+KERNEL_ROUTE, KERNEL_SPLIT, KERNEL_STACK = 9, 10, 11
 KERNEL_NAMES = {0: "moe_up", 1: "gate_up", 2: "moe_down", 3: "down_slots", 4: "topk",
                 5: "permute", 6: "grouped_gate_up", 7: "grouped_down", 8: "combine", 9: "route",
-                10: "split"}
+                10: "split", 11: "decode_stack"}
 
 _lib = None
 
@@ -187,6 +188,15 @@ class Context:
     def moe_decode(self, shape, layer, hidden: int, n_tokens: int, ids: int = 0, weights: int = 0):
         self._check(self.lib.smoe_hip_moe_decode(self.ptr, C.byref(shape), C.byref(layer), hidden,
                                                  n_tokens, ids or None, weights or None), "moe_decode")
+
+    def moe_decode_stack(self, shape, layers, hidden: int, ids: int = 0, weights: int = 0):
+        """layers: a sequence of SmoeMoeLayer (or a ctypes array of them)."""
+        if not isinstance(layers, C.Array):
+            arr = (SmoeMoeLayer * len(layers))(*layers)
+        else:
+            arr = layers
+        self._check(self.lib.smoe_hip_moe_decode_stack(self.ptr, C.byref(shape), arr, len(arr), hidden,
+                                                       ids or None, weights or None), "moe_decode_stack")
 
     def moe_prefill(self, shape, layer, hidden: int, n_tokens: int, ids: int = 0, weights: int = 0,
                     expert_offsets: int = 0, sorted_tokens: int = 0, union_ids: int = 0,
