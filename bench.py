@@ -88,9 +88,10 @@ def main():
     ap.add_argument("--replicas", type=int, default=4, help="prefill/batched: layer replicas rotated")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (0: config's)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
-    ap.add_argument("--engine", default="layers", choices=("stack", "layers"),
-                    help="stack: the whole step in one persistent launch (smoe_hip_moe_decode_stack); "
-                         "layers: two launches per layer (smoe_hip_moe_decode)")
+    ap.add_argument("--engine", default="stack", choices=("stack", "persistent", "layers"),
+                    help="stack: smoe_hip_moe_decode_stack with two launches per layer; persistent: smoe_hip_moe_decode_stack with "
+                         "the whole step in one persistent launch; layers: one smoe_hip_moe_decode call per "
+                         "layer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU work the baseline sample aims at")
     ap.add_argument("--profile-steps", type=int, default=8, help="replays of the event-timed step (0: skip)")
@@ -143,7 +144,12 @@ def main():
     off, raw, stride = smoe_amd.blob_layout(D, I)
     log(f"generating {NL} layers x {E} experts ({NL * E * stride / 1e9:.1f} GB) on the GPU")
     pool = torch.empty(NL * E * stride, dtype=torch.uint8, device=dev)
-    ctx.synth_expert_pool(pool.data_ptr(), 0, NL, E, stride, shape, SEED, 0.02)
+    t_gen = time.perf_counter()
+    for l0 in range(0, NL, 8):            # in chunks, with progress lines
+        n = min(8, NL - l0)
+        ctx.synth_expert_pool(pool.data_ptr() + l0 * E * stride, l0, n, E, stride, shape, SEED, 0.02)
+        torch.cuda.synchronize()
+        log(f"  layers {l0}..{l0 + n - 1} generated ({time.perf_counter() - t_gen:.1f} s)")
     router = torch.empty((NL, E * D), dtype=torch.int16, device=dev)
     for l in range(NL):
         ctx.synth_bf16(router[l].data_ptr(), E * D, SEED, smoe_amd.router_stream(l), 0.02)
@@ -157,7 +163,9 @@ def main():
     torch.cuda.synchronize()
     layer_arr = (smoe_amd.SmoeMoeLayer * NL)(*layers)
 
-    if args.engine == "stack":
+    if args.engine in ("stack", "persistent"):
+        ctx.set_decode_engine(smoe_amd.DECODE_PERSISTENT if args.engine == "persistent" else smoe_amd.DECODE_LAUNCHES)
+
         def step():
             ctx.moe_decode_stack(shape, layer_arr, hidden.data_ptr())
     else:
@@ -208,7 +216,9 @@ def main():
         "config": {"workload": c["workload"], "d_model": D, "n_experts": E, "top_k": K, "d_ff": I,
                    "layers": NL, "batch": 1, "decode_steps": args.steps,
                    "quant": "SMOE-Q4 g64 fp16 absmax", "launch": "hip-graph" if graph else "eager",
-                   "engine": "persistent stack kernel" if args.engine == "stack" else "two launches per layer",
+                   "engine": {"stack": "stack API, two launches per layer",
+                              "persistent": "stack API, one persistent launch per step",
+                              "layers": "one decode call per layer"}[args.engine],
                    "resident_expert_bytes": NL * E * raw},
     }
 
@@ -298,7 +308,7 @@ def cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, targ
                 gpu_h.copy_(torch.from_numpy(h))
                 lay = smoe_amd.make_layer(norm_w.data_ptr(), router[l].data_ptr(),
                                           pool.data_ptr() + l * layer_bytes, stride, off)
-                if engine == "stack":
+                if engine == "persistent":
                     ctx.moe_decode_stack(shape, [lay], gpu_h.data_ptr(), ids.data_ptr())
                 else:
                     ctx.moe_decode(shape, lay, gpu_h.data_ptr(), 1, ids.data_ptr())

@@ -235,17 +235,25 @@ int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
  * decode.cpp:121 over the block above, hidden [d_model] (device, in place)
  *   for l in 0 .. n_layers-1:  hidden += MoE_l(RMSNorm_l(hidden))
  * with layers [n_layers] a host array of layer descriptors (all of one shape).
- * The whole step is one persistent kernel launch (no per-layer kernel
- * boundary); results equal n_layers calls of smoe_hip_moe_decode up to fp32
- * summation order.  ids_out / weights_out [n_layers x top_k] are optional
- * device outputs (rank order, renormalised, decode.cpp:285-307).  The layer
- * table is copied to the device when it differs from the previous call's
- * (outside graph capture; under capture a new table gives SMOE_ERR_CAPTURE).
- * Shapes the persistent kernel does not cover (d_model > 4096, d_ff > 2048,
- * more than 512 experts) run as n_layers smoe_hip_moe_decode calls. */
+ * ids_out / weights_out [n_layers x top_k] are optional device outputs (rank
+ * order, renormalised, decode.cpp:285-307).  Two engines
+ * (smoe_hip_set_decode_engine):
+ *   SMOE_DECODE_LAUNCHES (default): two launches per layer, exactly
+ *     n_layers smoe_hip_moe_decode calls.
+ *   SMOE_DECODE_PERSISTENT: the whole step in one persistent kernel launch
+ *     (no per-layer kernel boundary); results equal the per-layer calls up to
+ *     fp32 summation order.  Its layer table is copied to the device when it
+ *     differs from the previous call's (outside graph capture; under capture
+ *     a new table gives SMOE_ERR_CAPTURE).  Shapes it does not cover
+ *     (d_model > 2048, d_ff > 2048, more than 512 experts) take the launches. */
 int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
                               const SmoeMoeLayer* layers, uint32_t n_layers, float* hidden,
                               uint32_t* ids_out, float* weights_out);
+
+#define SMOE_DECODE_LAUNCHES   0
+#define SMOE_DECODE_PERSISTENT 1
+/* Select the engine of smoe_hip_moe_decode_stack for this context. */
+int smoe_hip_set_decode_engine(SmoeMetalCtx* ctx, int engine);
 
 /* Prefill MoE block (prefill.cpp:308-453) over n_tokens rows [n_tokens x
  * d_model]: per token RMSNorm + router + top-k, then the layer-major expert

@@ -89,6 +89,7 @@ struct SmoeMetalCtx {
     DeviceScratch ds;
     PrefillScratch ps;
     StackScratch ss;
+    int decode_engine = SMOE_DECODE_LAUNCHES;   // smoe_hip_moe_decode_stack's engine
     uint32_t* d_err = nullptr;       // [1] device-side error flags (bit 0: exchange time-out, bit 1: bad expert id)
     uint32_t* perm_pairs = nullptr;  // smoe_hip_permute's sorted pair ids
     float* mv_in = nullptr;          // reference-surface GEMV staging
@@ -647,6 +648,13 @@ extern "C" int smoe_hip_synchronize(SmoeMetalCtx* ctx)
     return SMOE_OK;
 }
 
+extern "C" int smoe_hip_set_decode_engine(SmoeMetalCtx* ctx, int engine)
+{
+    if (!ctx || (engine != SMOE_DECODE_LAUNCHES && engine != SMOE_DECODE_PERSISTENT)) return SMOE_ERR_ARG;
+    ctx->decode_engine = engine;
+    return SMOE_OK;
+}
+
 extern "C" int smoe_hip_reserve(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, uint32_t max_tokens)
 {
     if (!ctx || !shape || max_tokens == 0) return SMOE_ERR_ARG;
@@ -700,8 +708,8 @@ extern "C" int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* 
     int rc = shape_check(shape);
     if (rc != SMOE_OK) return rc;
     const MoeDims d = dims_of(shape);
-    if (!smoe::stack_supported(d)) {
-        // outside the persistent kernel's shapes: one decode call per layer
+    if (ctx->decode_engine != SMOE_DECODE_PERSISTENT || !smoe::stack_supported(d)) {
+        // two launches per layer
         for (uint32_t l = 0; l < n_layers; ++l) {
             rc = moe_forward(ctx, shape, &layers[l], hidden, 1, ids_out ? ids_out + size_t(l) * d.K : nullptr,
                              weights_out ? weights_out + size_t(l) * d.K : nullptr);

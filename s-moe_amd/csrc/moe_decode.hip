@@ -61,19 +61,25 @@ void k_topk(const float* __restrict__ scores, uint32_t n, uint32_t k, uint32_t n
 // k_moe_up: RMSNorm + router + softmax/top-k + gate/up/SiLU for one layer.
 // One wave per block; grid (I / 8, K, T).  Lane l owns the 32 columns of
 // chunk l (+64 j) of the hidden dimension throughout.  Every wave:
-//   1. loads its hidden and norm-weight chunks (block b < E also router row b),
+//   1. loads its hidden and norm-weight chunks and its router rows,
 //   2. RMS-normalises them, normed = (x * inv) * w (common.hpp:245-256),
 //   3. turns the normed chunk into 4-bit digit words (Q4Act),
-//   4. block b < E: logit b = router_w[b] . normed (common.hpp:293-306),
-//      published as a flag-carrying 64-bit word,
+//   4. computes its router rows' logits, router_w[row] . normed
+//      (common.hpp:293-306), published as flag-carrying 64-bit words,
 //   5. polls the E logits of its token and selects the experts itself
 //      (softmax + top-k, scout.cpp:77-123; renormalised, decode.cpp:296-302),
 //   6. streams 8 rows of gate and up of the expert of rank blockIdx.y and
 //      writes h = silu(gate) * up (kernels.metal:240-337).
-// Producers have the lowest block ids of their token, so they are dispatched
-// before any consumer that waits on them; a bounded spin reports a timeout
-// (err) instead of hanging.  Block 0 of each token publishes ids, weights
-// and the expert table.  Steps 1-3 overlap the router rows' latency.
+// The logit exchange is XCD-local when the token's block count is a multiple
+// of 8: the dispatcher deals consecutive blocks round-robin over the 8 XCDs
+// (from some starting XCD), so block b is the (b/8)-th of its XCD, and the
+// blocks of every XCD compute all E rows among themselves (rows b/8,
+// b/8 + nb/8, ...).  The words then stay in that XCD's L2 (plain stores; the
+// pollers' loads are agent-scope) in the copy of its XCC_ID.  Otherwise block
+// b < E computes rows b, b + nb, ... and writes every copy through.  A bounded
+// spin reports a timeout (err) instead of hanging.  Block 0 of each token
+// publishes ids, weights and the expert table.  Steps 1-3 overlap the router
+// rows' latency.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint64_t ll_word(float v) { return (1ull << 32) | __float_as_uint(v); }
 
@@ -81,21 +87,36 @@ constexpr uint32_t SPIN_LIMIT = 1u << 22;
 constexpr int UP_RB = 8;   // rows per wave
 constexpr int SMOE_G = 64; // SMOE-Q4 group size (shatter_moe.py Q2_GROUP_SIZE)
 
-template <int CPL, int VPL, bool PRODUCER>
+template <int CPL, int VPL, bool LOCAL>
 __device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L, const float* __restrict__ hv,
                                             uint64_t* __restrict__ ll, float* __restrict__ h,
                                             uint32_t* __restrict__ ids_out, float* __restrict__ w_out,
-                                            ExpertPtrs* __restrict__ tbl_out, uint32_t* __restrict__ err,
-                                            uint32_t b)
+                                            ExpertPtrs* __restrict__ tbl_out, uint32_t* __restrict__ err)
 {
     constexpr int RB = UP_RB;
     const int lane = threadIdx.x;
     const uint32_t tok = blockIdx.z, r = blockIdx.y;
     const uint32_t D = d.D, nch = D >> 5;
+    const uint32_t nb = gridDim.x * gridDim.y;
+    const uint32_t b = blockIdx.y * gridDim.x + blockIdx.x;
+    uint32_t row0, rstep, copy;
+    if constexpr (LOCAL) {
+        uint32_t xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(xcc));
+        row0 = b >> 3;
+        rstep = nb >> 3;
+        copy = xcc & (LL_COPIES - 1);
+    } else {
+        row0 = b;
+        rstep = nb;
+        copy = b % LL_COPIES;
+    }
+    const bool producer = row0 < d.E;
+    const bool second = row0 + rstep < d.E;
 
     // 1. chunk loads (router last, so the norm can start before it lands)
     float4 x[CPL][8];
-    uint4 g[CPL][4], rw[CPL][4];
+    uint4 g[CPL][4], rw[CPL][4], rw2[CPL][4];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const uint32_t c = min(lane + WAVE * j, nch - 1);
@@ -104,13 +125,24 @@ __device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L
 #pragma unroll
         for (int q = 0; q < 4; ++q) g[j][q] = load_u4(L.norm_w + c * 32 + q * 8);
     }
-    if constexpr (PRODUCER) {
-        const uint16_t* wr = L.router_w + static_cast<size_t>(b) * D;
+    // router rows: plain loads (the previous layer's down kernel may have
+    // left them in this XCD's L2)
+    if (producer) {
+        const uint16_t* wr = L.router_w + static_cast<size_t>(row0) * D;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const uint32_t c = min(lane + WAVE * j, nch - 1);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) rw[j][q] = load_stream_u4(wr + c * 32 + q * 8);
+            for (int q = 0; q < 4; ++q) rw[j][q] = load_u4(wr + c * 32 + q * 8);
+        }
+        if (second) {
+            const uint16_t* wr2 = L.router_w + static_cast<size_t>(row0 + rstep) * D;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) rw2[j][q] = load_u4(wr2 + c * 32 + q * 8);
+            }
         }
     }
     // 2. RMS norm over the wave's D columns
@@ -143,46 +175,57 @@ __device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L
             a[j][4 * q + 3] = (x[j][q].w * inv) * bf16_to_f32(g1 >> 16);
         }
     }
-    // 3. digit form of the normed chunk
-    Q4Act qa[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) q4_act_from_floats(a[j], qa[j]);
-    // 4. router rows b, b + nb, ... (nb blocks per token; padding lanes hold normed 0)
-    if constexpr (PRODUCER) {
-        const uint32_t nb = gridDim.x * gridDim.y;
-        for (uint32_t row = b;;) {
-            float acc = 0.f;
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint32_t w4[4] = {rw[j][q].x, rw[j][q].y, rw[j][q].z, rw[j][q].w};
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        acc = fmaf(bf16_to_f32(w4[t] & 0xFFFFu), a[j][8 * q + 2 * t], acc);
-                        acc = fmaf(bf16_to_f32(w4[t] >> 16), a[j][8 * q + 2 * t + 1], acc);
-                    }
-                }
-            }
-            acc = wave_sum(acc);
+    // 4. router rows row0, row0 + rstep, ... (padding lanes hold normed 0)
+    uint64_t* llc = ll + copy * ll_copy_words(d.E);
+    auto publish = [&](uint32_t row, float acc) {
+        if constexpr (LOCAL) {
+            if (lane == 0)
+                __hip_atomic_store(llc + row, ll_word(acc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+        } else {
             if (lane < static_cast<int>(LL_COPIES))
                 __hip_atomic_store(ll + lane * ll_copy_words(d.E) + row, ll_word(acc), __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
-            row += nb;
-            if (row >= d.E) break;
-            const uint16_t* wr = L.router_w + static_cast<size_t>(row) * D;
+        }
+    };
+    auto row_dot = [&](const uint4 (&w)[CPL][4]) {
+        float acc = 0.f;
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                const uint32_t c = min(lane + WAVE * j, nch - 1);
+        for (int j = 0; j < CPL; ++j) {
 #pragma unroll
-                for (int q = 0; q < 4; ++q) rw[j][q] = load_stream_u4(wr + c * 32 + q * 8);
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t w4[4] = {w[j][q].x, w[j][q].y, w[j][q].z, w[j][q].w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    acc = fmaf(bf16_to_f32(w4[t] & 0xFFFFu), a[j][8 * q + 2 * t], acc);
+                    acc = fmaf(bf16_to_f32(w4[t] >> 16), a[j][8 * q + 2 * t + 1], acc);
+                }
+            }
+        }
+        return wave_sum(acc);
+    };
+    if (producer) {
+        publish(row0, row_dot(rw));
+        if (second) {
+            publish(row0 + rstep, row_dot(rw2));
+            for (uint32_t row = row0 + 2 * rstep; row < d.E; row += rstep) {
+                const uint16_t* wr = L.router_w + static_cast<size_t>(row) * D;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) rw[j][q] = load_u4(wr + c * 32 + q * 8);
+                }
+                publish(row, row_dot(rw));
             }
         }
     }
+    // 3. digit form of the normed chunk (overlaps the logit exchange)
+    Q4Act qa[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) q4_act_from_floats(a[j], qa[j]);
     // 5. wait for the E logits (in this block's copy), then select
     float v[VPL];
     {
-        const uint64_t* llc = ll + (b % LL_COPIES) * ll_copy_words(d.E);
         uint32_t spins = 0;
         bool all;
         do {
@@ -227,7 +270,7 @@ __device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L
     }
 
     // 6. 8 rows of gate and up: every weight load in flight before any is used
-    const uint32_t row0 = blockIdx.x * RB;
+    const uint32_t rowg = blockIdx.x * RB;
     const uint8_t* blob = L.experts + static_cast<size_t>(expert) * L.stride;
     const uint8_t* pa = blob + L.off[0];
     const uint16_t* sa = reinterpret_cast<const uint16_t*>(blob + L.off[1]);
@@ -238,7 +281,7 @@ __device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L
     uint16_t sva[RB][CPL], svb[RB][CPL];
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
-        const size_t row = row0 + i;
+        const size_t row = rowg + i;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const uint32_t c = min(lane + WAVE * j, nch - 1);
@@ -269,10 +312,10 @@ __device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L
     const float uv = __shfl(tot, (2 * lane + 1) << SH);
     // silu(z) = z * (1 / (1 + exp(-z)))  (kernels.metal:61-63, :334-336), all rows at once
     float* o = h + (static_cast<size_t>(tok) * d.K + r) * d.I;
-    if (lane < RB) o[row0 + lane] = (gv * (1.0f / (1.0f + expf(-gv)))) * uv;
+    if (lane < RB) o[rowg + lane] = (gv * (1.0f / (1.0f + expf(-gv)))) * uv;
 }
 
-template <int CPL, int VPL>
+template <int CPL, int VPL, bool LOCAL>
 __global__ __launch_bounds__(WAVE)
 void k_moe_up(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint64_t* __restrict__ ll_all,
               float* __restrict__ h, uint32_t* __restrict__ ids_out, float* __restrict__ w_out,
@@ -281,11 +324,7 @@ void k_moe_up(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint64_t
     const uint32_t tok = blockIdx.z;
     const float* hv = hidden + static_cast<size_t>(tok) * d.D;
     uint64_t* ll = ll_all + static_cast<size_t>(tok) * ll_token_words(d.E);
-    const uint32_t b = blockIdx.y * gridDim.x + blockIdx.x;
-    if (b < d.E)
-        moe_up_body<CPL, VPL, true>(d, L, hv, ll, h, ids_out, w_out, tbl_out, err, b);
-    else
-        moe_up_body<CPL, VPL, false>(d, L, hv, ll, h, ids_out, w_out, tbl_out, err, b);
+    moe_up_body<CPL, VPL, LOCAL>(d, L, hv, ll, h, ids_out, w_out, tbl_out, err);
 }
 
 // ---------------------------------------------------------------------------
@@ -492,14 +531,29 @@ void k_down_combine(MoeDims d, const ExpertPtrs* __restrict__ tbl, const float* 
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
+template <int CPL, int VPL>
+static void moe_up_v(dim3 grid, hipStream_t s, const MoeDims& d, const LayerDesc& L, const float* hidden,
+                     uint64_t* ll, float* h, uint32_t* ids, float* w, ExpertPtrs* tbl, uint32_t* err)
+{
+    // XCD-local logit exchange when every XCD receives the same number of
+    // blocks of each token, they cover the router rows in at most two each,
+    // and the whole grid is resident at once (the dispatcher's round-robin
+    // over the XCDs is then unbroken)
+    const uint32_t nb = grid.x * grid.y;
+    if (nb % 8 == 0 && nb / 8 * 2 >= d.E && nb * grid.z <= 1024)
+        launch_kernel(k_moe_up<CPL, VPL, true>, grid, dim3(WAVE), s, d, L, hidden, ll, h, ids, w, tbl, err);
+    else
+        launch_kernel(k_moe_up<CPL, VPL, false>, grid, dim3(WAVE), s, d, L, hidden, ll, h, ids, w, tbl, err);
+}
+
 template <int CPL>
 static void moe_up_c(dim3 grid, hipStream_t s, const MoeDims& d, const LayerDesc& L, const float* hidden,
                      uint64_t* ll, float* h, uint32_t* ids, float* w, ExpertPtrs* tbl, uint32_t* err)
 {
     if (d.E <= 128)
-        launch_kernel(k_moe_up<CPL, 2>, grid, dim3(WAVE), s, d, L, hidden, ll, h, ids, w, tbl, err);
+        moe_up_v<CPL, 2>(grid, s, d, L, hidden, ll, h, ids, w, tbl, err);
     else
-        launch_kernel(k_moe_up<CPL, 8>, grid, dim3(WAVE), s, d, L, hidden, ll, h, ids, w, tbl, err);
+        moe_up_v<CPL, 8>(grid, s, d, L, hidden, ll, h, ids, w, tbl, err);
 }
 
 hipError_t launch_moe_up(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t n_tok, uint64_t* ll,
@@ -585,9 +639,15 @@ hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const fl
     if (nw > DOWN_MAX_WAVES || d.D % DOWN_RB) return hipErrorInvalidValue;
     dim3 grid(d.D / DOWN_RB, n_tok), block(nw * WAVE);
     switch (ppl) {
-        case 1: launch_kernel(k_down_combine<1>, grid, block, s, d, tbl, h, w, hidden, ll); break;
-        case 2: launch_kernel(k_down_combine<2>, grid, block, s, d, tbl, h, w, hidden, ll); break;
-        default: launch_kernel(k_down_combine<4>, grid, block, s, d, tbl, h, w, hidden, ll); break;
+        case 1:
+            launch_kernel(k_down_combine<1>, grid, block, s, d, tbl, h, w, hidden, ll);
+            break;
+        case 2:
+            launch_kernel(k_down_combine<2>, grid, block, s, d, tbl, h, w, hidden, ll);
+            break;
+        default:
+            launch_kernel(k_down_combine<4>, grid, block, s, d, tbl, h, w, hidden, ll);
+            break;
     }
     return hipGetLastError();
 }

@@ -95,6 +95,34 @@ __device__ __forceinline__ void poll_until(F&& round, uint32_t* err, bool& dead)
     }
 }
 
+// A wave-uniform copy of a descriptor read from LDS (scalar registers: the
+// weight loads then take a scalar base and a 32-bit lane offset).
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p)
+{
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v)
+{
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ LayerDesc uniform_desc(const LayerDesc& s)
+{
+    LayerDesc d;
+    d.norm_w = uniform_ptr(s.norm_w);
+    d.router_w = uniform_ptr(s.router_w);
+    d.experts = uniform_ptr(s.experts);
+    d.stride = uniform_u64(s.stride);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) d.off[i] = uniform_u64(s.off[i]);
+    return d;
+}
+
 // LDS float4 index of quad q of 32-value chunk c (f = 8 c + q), rotated so
 // that 64 lanes reading quad q of chunks lane, lane + 64, ... spread over the
 // banks.
@@ -151,8 +179,10 @@ void k_decode_stack(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_
     __shared__ float4 h_s[CW * 8];
     __shared__ LayerDesc tbl_s[ST_MAX_LAYERS];
     __shared__ uint2 topk_s[ST_WPB][TOPK_SLOTS];
+    __shared__ float y_s[SMOE_TOPK_MAX_K][ST_WPB * 16];   // the block's combine rows, all ranks
 
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // wv is wave-uniform: readfirstlane lets row and address arithmetic stay scalar
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     // Role of this block: XCD x and index jb among that XCD's 32 blocks.  The
     // dispatcher deals blocks round-robin over the 8 XCDs, but not always
     // starting at XCD 0, so each block takes the XCD it runs on (XCC_ID) and a
@@ -230,10 +260,10 @@ void k_decode_stack(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_
                 for (int q = 0; q < 4; ++q) gw[j][q] = load_u4(Ld.norm_w + c * 32 + q * 8);
             }
         };
-        fetch_router(tbl_s[0]);
+        fetch_router(uniform_desc(tbl_s[0]));
 
         for (uint32_t l = 0; l < n_layers; ++l) {
-            const LayerDesc Ld = tbl_s[l];
+            const LayerDesc Ld = uniform_desc(tbl_s[l]);
             const uint32_t ep = ep0 + l + 1;
 
             // ---- H: the layer's input hidden into LDS ------------------------
@@ -343,7 +373,16 @@ void k_decode_stack(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_
             // digit form of the normed chunks (overlaps the logit exchange)
             Q4Act qa[CPL];
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) q4_act_from_floats(a[j], qa[j]);
+            for (int j = 0; j < CPL; ++j) {
+                q4_act_from_floats(a[j], qa[j]);
+                // materialise the digits here, before the poll loop below, so
+                // the conversion overlaps the wait instead of following it
+#pragma unroll
+                for (int dd = 0; dd < Q4_DIGITS; ++dd)
+                    asm volatile("" ::"v"(qa[j].dig[dd][0]), "v"(qa[j].dig[dd][1]), "v"(qa[j].dig[dd][2]),
+                                 "v"(qa[j].dig[dd][3]));
+                asm volatile("" ::"v"(qa[j].xsum_half), "v"(qa[j].kscale));
+            }
 
             // ---- T: the XCD's E logits, softmax + top-k ----------------------
             float v[VPL];
@@ -425,7 +464,7 @@ void k_decode_stack(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_
                 if (d0 < d1) load_down(0);
                 __builtin_amdgcn_sched_barrier(0);
                 if (!prefetched) {
-                    fetch_router(tbl_s[l + 1]);
+                    fetch_router(uniform_desc(tbl_s[l + 1]));
                     prefetched = true;
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -519,37 +558,53 @@ void k_decode_stack(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_
                 }
                 __syncthreads();   // h_s is refilled by the next rank
             }
-            if (!prefetched) fetch_router(tbl_s[l + 1]);
+            if (!prefetched) fetch_router(uniform_desc(tbl_s[l + 1]));
 
             // ---- C: hidden + sum_r w_r y_r for rows [jw rpc, ...) -----------
+            // The y words come from every XCD: one wave per block polls the
+            // block's rows of all ranks (a quarter of the cross-XCD requests
+            // of every wave polling its own) and hands them over through LDS.
             {
-                const uint32_t rpc = (D + ST_WX - 1) / ST_WX;
+                const uint32_t rpc = (D + ST_WX - 1) / ST_WX;          // rows per wave (<= 16)
+                const uint32_t brow0 = (jw - wv) * rpc;                 // the block's first row
+                if (wv == 0) {
+                    const uint32_t br = brow0 + lane;
+                    const bool mine = static_cast<uint32_t>(lane) < ST_WPB * rpc && br < D;
+                    const uint32_t brc = min(br, D - 1);
+                    float y[SMOE_TOPK_MAX_K];
+                    poll_until(
+                        [&] {
+                            bool ok = true;
+                            if (mine) {
+#pragma unroll
+                                for (int r = 0; r < SMOE_TOPK_MAX_K; ++r) {
+                                    if (static_cast<uint32_t>(r) < K) {
+                                        const uint64_t w = get_word(YR(l, r) + brc);
+                                        y[r] = word_value(w);
+                                        ok &= flag_is(w, ep);
+                                    }
+                                }
+                            }
+                            return ok;
+                        },
+                        err, dead);
+                    if (mine) {
+#pragma unroll
+                        for (int r = 0; r < SMOE_TOPK_MAX_K; ++r)
+                            if (static_cast<uint32_t>(r) < K) y_s[r][lane] = y[r];
+                    }
+                }
+                __syncthreads();
                 const uint32_t row = jw * rpc + lane;
                 const bool mine = static_cast<uint32_t>(lane) < rpc && row < D;
                 const uint32_t rowc = min(row, D - 1);
-                float y[SMOE_TOPK_MAX_K];
-                poll_until(
-                    [&] {
-                        bool ok = true;
-                        if (mine) {
-#pragma unroll
-                            for (int r = 0; r < SMOE_TOPK_MAX_K; ++r) {
-                                if (static_cast<uint32_t>(r) < K) {
-                                    const uint64_t w = get_word(YR(l, r) + rowc);
-                                    y[r] = word_value(w);
-                                    ok &= flag_is(w, ep);
-                                }
-                            }
-                        }
-                        return ok;
-                    },
-                    err, dead);
+                const uint32_t yi = min(wv * rpc + lane, ST_WPB * 16u - 1);
                 // routed_out += w_r * y_r in rank order (axpy_f32, common.hpp:346-349),
                 // then hidden += routed_out (decode.cpp:506-509)
                 float routed = 0.f;
 #pragma unroll
                 for (int r = 0; r < SMOE_TOPK_MAX_K; ++r)
-                    if (static_cast<uint32_t>(r) < K) routed = routed + readlane_f32(my_w, r) * y[r];
+                    if (static_cast<uint32_t>(r) < K) routed = routed + readlane_f32(my_w, r) * y_s[r][yi];
                 const float hnew = reinterpret_cast<const float*>(hid_s)[swz4(rowc >> 2) * 4 + (rowc & 3)] + routed;
                 if (l + 1 < n_layers) {
                     if (mine) put_word_xcd(HID(l + 1) + row, ep + 1, hnew, local);

@@ -132,9 +132,12 @@ __device__ __forceinline__ void quantize_group(const float (&w)[G], uint8_t* pac
     for (int q = 0; q < G / 8; ++q) words[q] = 0;
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-        float q = __fdiv_rn(w[j], best);
-        q = __fmul_rn(q, 7.5f);
-        q = __fadd_rn(q, 7.5f);
+        // three separately rounded operations, as numpy's w / absmax * 7.5 + 7.5
+        // (written as operators under this file's contract(off): the header
+        // helpers __fmul_rn / __fadd_rn would still be fused into one fma)
+        float q = w[j] / best;
+        q = q * 7.5f;
+        q = q + 7.5f;
         int c = static_cast<int>(rintf(q));
         c = c < 0 ? 0 : (c > 15 ? 15 : c);
         words[j / 8] |= static_cast<uint32_t>(c) << (4 * (j % 8));

@@ -83,6 +83,7 @@ SIGNATURES = [
     ("smoe_hip_reserve", _I, [_VP, _SHP, _U32]),
     ("smoe_hip_moe_decode", _I, [_VP, _SHP, _LAY, _VP, _U32, _VP, _VP]),
     ("smoe_hip_moe_decode_stack", _I, [_VP, _SHP, _LAY, _U32, _VP, _VP, _VP]),
+    ("smoe_hip_set_decode_engine", _I, [_VP, _I]),
     ("smoe_hip_moe_prefill", _I, [_VP, _SHP, _LAY, _VP, _U32, _VP, _VP, _VP, _VP, _VP, _VP]),
     ("smoe_hip_compute_top_k", _I, [_VP, _VP, _U32, _U32, _U32, _VP, _VP, _I]),
     ("smoe_hip_permute", _I, [_VP, _VP, _VP, _U32, _U32, _U32, _VP, _VP, _VP, _VP, _VP]),
@@ -98,6 +99,7 @@ SIGNATURES = [
 KERNEL_MOE_UP, KERNEL_GATE_UP, KERNEL_MOE_DOWN, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
 KERNEL_PERMUTE, KERNEL_GROUPED_GATE_UP, KERNEL_GROUPED_DOWN, KERNEL_SCATTER = 5, 6, 7, 8
 KERNEL_ROUTE, KERNEL_SPLIT, KERNEL_STACK = 9, 10, 11
+DECODE_LAUNCHES, DECODE_PERSISTENT = 0, 1
 KERNEL_NAMES = {0: "moe_up", 1: "gate_up", 2: "moe_down", 3: "down_slots", 4: "topk",
                 5: "permute", 6: "grouped_gate_up", 7: "grouped_down", 8: "combine", 9: "route",
                 10: "split", 11: "decode_stack"}
@@ -188,6 +190,10 @@ class Context:
     def moe_decode(self, shape, layer, hidden: int, n_tokens: int, ids: int = 0, weights: int = 0):
         self._check(self.lib.smoe_hip_moe_decode(self.ptr, C.byref(shape), C.byref(layer), hidden,
                                                  n_tokens, ids or None, weights or None), "moe_decode")
+
+    def set_decode_engine(self, engine: int):
+        """DECODE_LAUNCHES (two launches per layer) or DECODE_PERSISTENT (one launch per step)."""
+        self._check(self.lib.smoe_hip_set_decode_engine(self.ptr, engine), "set_decode_engine")
 
     def moe_decode_stack(self, shape, layers, hidden: int, ids: int = 0, weights: int = 0):
         """layers: a sequence of SmoeMoeLayer (or a ctypes array of them)."""

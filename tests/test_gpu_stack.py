@@ -1,6 +1,7 @@
 """The whole-stack decode step (smoe_hip_moe_decode_stack: the decode.cpp:121
-layer loop in one persistent launch) against the CPU oracle of
-decode.cpp:236-509, layer by layer.  Top-k ids must be bit-exact; the MoE
+layer loop) against the CPU oracle of decode.cpp:236-509, layer by layer, for
+both engines: one persistent launch per step, and two launches per layer with
+the next layer's router read ahead.  Top-k ids must be bit-exact; the MoE
 delta and the post-residual hidden state within 1e-3 per element (rel_err
 metric).  A multi-layer call must equal the same layers run one call at a time
 bit for bit (each layer's input is the previous layer's fp32 output either
@@ -9,10 +10,19 @@ import numpy as np
 import pytest
 import torch
 
+import smoe_amd
 from gpu_helpers import Layer, hidden_states, moe_delta_err, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
+ENGINES = [smoe_amd.DECODE_PERSISTENT, smoe_amd.DECODE_LAUNCHES]
+
+
+@pytest.fixture(params=ENGINES, ids=["persistent", "launches"])
+def engine(ctx, request):
+    ctx.set_decode_engine(request.param)
+    yield request.param
+    ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
 
 
 def run_stack(ctx, layers, hid):
@@ -44,7 +54,7 @@ def check_layer(oracle, layer, h_in, h_out, gids, gw):
     (512, 128, 16, 256, False),    # two ranks per XCD, no renormalisation
     (1024, 512, 8, 1024, True),
 ])
-def test_stack_single_layer_vs_oracle(ctx, oracle, D, E, K, I, norm):
+def test_stack_single_layer_vs_oracle(ctx, oracle, engine, D, E, K, I, norm):
     layer = Layer(ctx, D, E, K, I, layer_id=D + E + K, norm_topk=norm)
     for index0 in (0, 5):
         hid = hidden_states(ctx, 1, D, index0)[0]
@@ -65,7 +75,7 @@ def test_stack_235b_layer(ctx, oracle):
     assert check_layer(oracle, layer, h0, hid.cpu().numpy(), gids[0], gw[0]) <= TOL
 
 
-def test_stack_235b_shape_per_layer_path(ctx, oracle):
+def test_stack_235b_shape_per_layer_path(ctx, oracle, engine):
     """Config 3 shape through smoe_hip_moe_decode_stack: shapes outside the
     persistent kernel run as per-layer decode calls, two layers here, each
     checked against the oracle on the GPU's own input."""
@@ -82,7 +92,7 @@ def test_stack_235b_shape_per_layer_path(ctx, oracle):
     assert torch.equal(full, step)
 
 
-def test_stack_multi_layer_teacher_forced(ctx, oracle):
+def test_stack_multi_layer_teacher_forced(ctx, oracle, engine):
     """Four 30B-shaped layers in one call: bit-identical to four one-layer
     calls, and every layer within the tolerance of the oracle applied to the
     GPU's own input of that layer."""
@@ -101,9 +111,10 @@ def test_stack_multi_layer_teacher_forced(ctx, oracle):
     assert worst <= TOL
 
 
-def test_stack_matches_per_layer_decode(ctx):
-    """The stack kernel and the two-launch decode path implement one MoE
-    block: same ids, hidden states within the tolerance of each other."""
+def test_stack_matches_per_layer_decode(ctx, engine):
+    """The stack call and per-layer smoe_hip_moe_decode calls implement one
+    MoE block: same ids, hidden states within the tolerance of each other
+    (bit-identical for the launch engine, which runs the same kernels)."""
     layers = [Layer(ctx, 2048, 128, 8, 768, layer_id=30 + i, host=False) for i in range(3)]
     x0 = hidden_states(ctx, 1, 2048, 12)[0]
     a = x0.clone()
@@ -114,13 +125,15 @@ def test_stack_matches_per_layer_decode(ctx):
         ctx.moe_decode(l.shape, l.layer, b.data_ptr(), 1, ids[i].data_ptr())
     ctx.synchronize()
     assert (ids.cpu().numpy().view(np.uint32) == fids).all()
+    if engine == smoe_amd.DECODE_LAUNCHES:
+        assert torch.equal(a, b)
     x = x0.cpu().numpy().astype(np.float64)
     da, db = a.cpu().numpy() - x, b.cpu().numpy() - x
     slack = np.spacing(np.abs(a.cpu().numpy())) + np.spacing(np.abs(b.cpu().numpy()))
     assert rel_err(da, db, slack=slack)[0] <= 3 * 2 * TOL
 
 
-def test_stack_repeated_calls_and_graph_replay(ctx):
+def test_stack_repeated_calls_and_graph_replay(ctx, engine):
     """Calls in a row (the exchange flags advance per call and are never
     re-armed) and replays of a captured graph with eager work in between all
     reproduce the first call exactly."""

@@ -39,7 +39,22 @@ def test_quantize_bit_exact_with_edge_groups(ctx, oracle):
     assert (ds.cpu().numpy().view(np.uint16) == s).all()
 
 
-@pytest.mark.parametrize("D,I", [(64, 64), (2048, 768)])
+def test_quantize_bit_exact_many_groups(ctx, oracle):
+    """16M weights: enough for values within an ulp of a rounding boundary of
+    w / absmax * 7.5 + 7.5, where fusing the multiply and the add into one
+    fma (a single rounding) would change a code."""
+    w = oracle.gen_normal(1 << 24, 3, 4242, 0.02)
+    dw = torch.from_numpy(w).cuda()
+    dp = torch.zeros(w.size // 2, dtype=torch.uint8, device="cuda")
+    ds = torch.zeros(w.size // 64, dtype=torch.int16, device="cuda")
+    ctx.quantize_q4(dw.data_ptr(), w.size, 64, dp.data_ptr(), ds.data_ptr())
+    p, s = oracle.quantize_q4(w)
+    assert (ds.cpu().numpy().view(np.uint16) == s).all()
+    bad = np.nonzero(dp.cpu().numpy() != p)[0]
+    assert bad.size == 0, (bad.size, bad[:4])
+
+
+@pytest.mark.parametrize("D,I", [(64, 64), (2048, 768), (4096, 1536)])
 def test_expert_pool_bit_exact(ctx, oracle, D, I):
     shape = smoe_amd.make_shape(D, 4, 2, I)
     off, raw, stride = smoe_amd.blob_layout(D, I)
