@@ -38,7 +38,8 @@ CONFIGS = {
 }
 HBM_PEAK_GBS = 8000.0
 SEED = 20261201
-KERNEL_SYMBOLS = {"moe_up": "k_moe_up", "moe_down": "k_down_combine", "decode_stack": "k_decode_stack"}
+KERNEL_SYMBOLS = {"moe_up": "k_moe_up", "moe_down": "k_down_combine", "decode_stack": "k_decode_stack",
+                  "moe_layer": "k_moe_layer"}
 
 
 def log(msg):
@@ -47,13 +48,15 @@ def log(msg):
 
 def kernel_bytes(c):
     """Algorithmic HBM bytes per launch of each decode kernel: one token-layer
-    for the two-launch path; one token through every layer for the stack
-    kernel (per layer k * B_expert + 2 E D router + 12 D for x, hidden in and
-    hidden out)."""
+    for the one- and two-launch paths; one token through every layer for the
+    stack kernel (per layer k * B_expert + 2 E D router + 12 D for x, hidden in
+    and hidden out)."""
     D, E, K, I = c["D"], c["E"], c["K"], c["I"]
     mat = D * I // 2 + D * I // 64 * 2            # packed nibbles + fp16 scales of one matrix
     return {
         "decode_stack": c["layers"] * (K * 3 * mat + 2 * E * D + 12 * D),
+        # the whole block: router bf16 + norm weights + 8 experts' gate/up/down + hidden in and out
+        "moe_layer": K * 3 * mat + 2 * E * D + 2 * D + 8 * D,
         # router bf16 + norm weights + hidden in + 8 experts' gate+up + h out
         "moe_up": E * D * 2 + D * 2 + D * 4 + K * 2 * mat + K * I * 4,
         # 8 experts' down + h in + weights + hidden read and written
@@ -88,10 +91,10 @@ def main():
     ap.add_argument("--replicas", type=int, default=4, help="prefill/batched: layer replicas rotated")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (0: config's)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
-    ap.add_argument("--engine", default="stack", choices=("stack", "persistent", "layers"),
-                    help="stack: smoe_hip_moe_decode_stack with two launches per layer; persistent: smoe_hip_moe_decode_stack with "
-                         "the whole step in one persistent launch; layers: one smoe_hip_moe_decode call per "
-                         "layer")
+    ap.add_argument("--engine", default="stack", choices=("stack", "split", "persistent", "layers"),
+                    help="stack: smoe_hip_moe_decode_stack, per-layer launches (one per layer where the shape "
+                         "allows); split: the same with two launches per layer; persistent: the whole step in "
+                         "one persistent launch; layers: one smoe_hip_moe_decode call per layer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU work the baseline sample aims at")
     ap.add_argument("--profile-steps", type=int, default=8, help="replays of the event-timed step (0: skip)")
@@ -163,8 +166,9 @@ def main():
     torch.cuda.synchronize()
     layer_arr = (smoe_amd.SmoeMoeLayer * NL)(*layers)
 
-    if args.engine in ("stack", "persistent"):
-        ctx.set_decode_engine(smoe_amd.DECODE_PERSISTENT if args.engine == "persistent" else smoe_amd.DECODE_LAUNCHES)
+    ctx.set_decode_engine({"persistent": smoe_amd.DECODE_PERSISTENT,
+                           "split": smoe_amd.DECODE_SPLIT}.get(args.engine, smoe_amd.DECODE_LAUNCHES))
+    if args.engine in ("stack", "split", "persistent"):
 
         def step():
             ctx.moe_decode_stack(shape, layer_arr, hidden.data_ptr())
@@ -216,7 +220,8 @@ def main():
         "config": {"workload": c["workload"], "d_model": D, "n_experts": E, "top_k": K, "d_ff": I,
                    "layers": NL, "batch": 1, "decode_steps": args.steps,
                    "quant": "SMOE-Q4 g64 fp16 absmax", "launch": "hip-graph" if graph else "eager",
-                   "engine": {"stack": "stack API, two launches per layer",
+                   "engine": {"stack": "stack API, per-layer launches",
+                              "split": "stack API, two launches per layer",
                               "persistent": "stack API, one persistent launch per step",
                               "layers": "one decode call per layer"}[args.engine],
                    "resident_expert_bytes": NL * E * raw},
@@ -267,7 +272,7 @@ def kernel_times(ctx, torch, stream, step, replays):
 def _read_profile(ctx, smoe_amd):
     out = {}
     for kid, name in ((smoe_amd.KERNEL_MOE_UP, "moe_up"), (smoe_amd.KERNEL_MOE_DOWN, "moe_down"),
-                      (smoe_amd.KERNEL_STACK, "decode_stack")):
+                      (smoe_amd.KERNEL_STACK, "decode_stack"), (smoe_amd.KERNEL_MOE_LAYER, "moe_layer")):
         n, ms = ctx.profile_read(kid)
         if n:
             out[name] = (n, ms * 1e3 / n)

@@ -226,7 +226,12 @@ int smoe_hip_reserve(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, uint32_t max_
  *   ids, w = top_k(softmax(logits)), renormalised   scout.cpp:77-123, decode.cpp:290-302
  *   hidden += sum_r w_r * FFN_{ids_r}(normed)       kernels.metal:308-365, decode.cpp:482-509
  * ids_out [n_tokens x top_k] and weights_out [n_tokens x top_k] are optional
- * device pointers.  Asynchronous on the context stream. */
+ * device pointers.  Asynchronous on the context stream.  One token with
+ * top_k = 8 (one selected expert per XCD of the MI355X) runs as a single
+ * kernel launch (SMOE_KERNEL_MOE_LAYER) when the shape's grid fits on the
+ * device at once; other calls, and every call under SMOE_DECODE_SPLIT, run
+ * two launches (SMOE_KERNEL_MOE_UP, SMOE_KERNEL_MOE_DOWN).  The two forms
+ * select the same experts and agree up to fp32 summation order. */
 int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
                         const SmoeMoeLayer* layer, float* hidden, uint32_t n_tokens,
                         uint32_t* ids_out, float* weights_out);
@@ -238,8 +243,9 @@ int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
  * ids_out / weights_out [n_layers x top_k] are optional device outputs (rank
  * order, renormalised, decode.cpp:285-307).  Two engines
  * (smoe_hip_set_decode_engine):
- *   SMOE_DECODE_LAUNCHES (default): two launches per layer, exactly
- *     n_layers smoe_hip_moe_decode calls.
+ *   SMOE_DECODE_LAUNCHES (default): exactly n_layers smoe_hip_moe_decode
+ *     calls (one or two launches per layer, as that entry point chooses).
+ *   SMOE_DECODE_SPLIT: the same calls, always two launches per layer.
  *   SMOE_DECODE_PERSISTENT: the whole step in one persistent kernel launch
  *     (no per-layer kernel boundary); results equal the per-layer calls up to
  *     fp32 summation order.  Its layer table is copied to the device when it
@@ -252,7 +258,9 @@ int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
 
 #define SMOE_DECODE_LAUNCHES   0
 #define SMOE_DECODE_PERSISTENT 1
-/* Select the engine of smoe_hip_moe_decode_stack for this context. */
+#define SMOE_DECODE_SPLIT      2
+/* Select the engine of smoe_hip_moe_decode_stack (and, for SMOE_DECODE_SPLIT,
+ * the form of smoe_hip_moe_decode) for this context. */
 int smoe_hip_set_decode_engine(SmoeMetalCtx* ctx, int engine);
 
 /* Prefill MoE block (prefill.cpp:308-453) over n_tokens rows [n_tokens x
@@ -330,6 +338,7 @@ int smoe_hip_synth_expert_pool(SmoeMetalCtx* ctx, uint8_t* base, uint32_t first_
 #define SMOE_KERNEL_ROUTE         9   /* prefill: RMSNorm + router + top-k per token          */
 #define SMOE_KERNEL_SPLIT        10   /* prefill: f16 hi/lo planes of activations             */
 #define SMOE_KERNEL_STACK        11   /* decode: every layer of a stack in one launch         */
+#define SMOE_KERNEL_MOE_LAYER    12   /* decode: the whole MoE block of one token in one launch */
 #define SMOE_KERNEL_KINDS        16
 int smoe_hip_profile_enable(SmoeMetalCtx* ctx, int enable);
 int smoe_hip_profile_read(SmoeMetalCtx* ctx, uint32_t kernel, uint64_t* launches, double* total_ms);

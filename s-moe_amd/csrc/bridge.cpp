@@ -34,6 +34,7 @@ struct DeviceScratch {
     float* w = nullptr;          // [T x K]
     ExpertPtrs* tbl = nullptr;   // [T x K]
     float* h = nullptr;          // [T x K x I]
+    uint64_t* lx = nullptr;      // one-launch layer exchange words (lx_words), zero at allocation
 };
 
 // prefill / permute scratch for one batch of up to T tokens (P = T * K pairs)
@@ -145,6 +146,7 @@ void free_device_scratch(DeviceScratch& s)
     dfree(s.w);
     dfree(s.tbl);
     dfree(s.h);
+    dfree(s.lx);
     s = DeviceScratch{};
 }
 
@@ -240,9 +242,13 @@ int ensure_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
     free_device_scratch(c);
     const size_t T_ = n.T;
     bool ok = dalloc(ctx, &n.ll, T_ * smoe::ll_token_words(n.E)) && dalloc(ctx, &n.ids, T_ * n.K) &&
-              dalloc(ctx, &n.w, T_ * n.K) && dalloc(ctx, &n.tbl, T_ * n.K) && dalloc(ctx, &n.h, T_ * n.K * n.I);
-    // the exchange words start disarmed; every launch pair leaves them so
-    ok = ok && hip_ok(ctx, hipMemset(n.ll, 0, T_ * smoe::ll_token_words(n.E) * sizeof(uint64_t)), "hipMemset");
+              dalloc(ctx, &n.w, T_ * n.K) && dalloc(ctx, &n.tbl, T_ * n.K) && dalloc(ctx, &n.h, T_ * n.K * n.I) &&
+              dalloc(ctx, &n.lx, smoe::lx_words(n.D, n.E, n.I));
+    // the exchange words start disarmed; every launch pair leaves them so.
+    // The one-launch words start at epoch 0 and are never re-armed: a fresh
+    // zero word can never carry a live tag (tags start at 1)
+    ok = ok && hip_ok(ctx, hipMemset(n.ll, 0, T_ * smoe::ll_token_words(n.E) * sizeof(uint64_t)), "hipMemset") &&
+         hip_ok(ctx, hipMemset(n.lx, 0, smoe::lx_words(n.D, n.E, n.I) * sizeof(uint64_t)), "hipMemset");
     if (!ok) {
         free_device_scratch(n);
         return SMOE_ERR_HIP;
@@ -650,7 +656,8 @@ extern "C" int smoe_hip_synchronize(SmoeMetalCtx* ctx)
 
 extern "C" int smoe_hip_set_decode_engine(SmoeMetalCtx* ctx, int engine)
 {
-    if (!ctx || (engine != SMOE_DECODE_LAUNCHES && engine != SMOE_DECODE_PERSISTENT)) return SMOE_ERR_ARG;
+    if (!ctx || (engine != SMOE_DECODE_LAUNCHES && engine != SMOE_DECODE_PERSISTENT && engine != SMOE_DECODE_SPLIT))
+        return SMOE_ERR_ARG;
     ctx->decode_engine = engine;
     return SMOE_OK;
 }
@@ -677,6 +684,14 @@ static int moe_forward(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, const SmoeM
     const LayerDesc L = layer_of(layer);
     uint32_t* ids = ids_out ? ids_out : s.ids;
     float* w = weights_out ? weights_out : s.w;
+    if (n_tokens == 1 && ctx->decode_engine != SMOE_DECODE_SPLIT && smoe::layer_supported(d)) {
+        if (!timed(ctx, SMOE_KERNEL_MOE_LAYER, "moe_layer", [&] {
+                return smoe::launch_moe_layer(d, L, hidden, s.lx, ids, w, ctx->d_err, ctx->stream);
+            }))
+            return SMOE_ERR_HIP;
+        ctx->dispatches.fetch_add(d.K, std::memory_order_relaxed);
+        return SMOE_OK;
+    }
     if (!timed(ctx, SMOE_KERNEL_MOE_UP, "moe_up", [&] {
             return smoe::launch_moe_up(d, L, hidden, n_tokens, s.ll, s.h, ids, w, s.tbl, ctx->d_err, ctx->stream);
         }))

@@ -87,6 +87,24 @@ hipError_t launch_gate_up(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n_ex
 // zeroes ll [T x (E+1)] for the next launch_moe_up
 hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const float* h, const float* w,
                                float* hidden, uint64_t* ll, uint32_t n_tok, hipStream_t s);
+// ---- decode, one token, one launch (moe_layer.hip) -----------------------
+// Exchange words of the one-launch layer: word 0 holds the epoch (the tag of
+// the last launch), then 8 logit copies of lx_pad(E) words, 8 h copies of
+// lx_pad(I) words and 8 rank partials of lx_pad(D) words.  Zero once at
+// allocation; never re-armed.
+constexpr uint32_t LX_HEAD = 64;
+constexpr uint32_t LX_MAX_I = 2048;
+__host__ __device__ constexpr uint32_t lx_pad(uint32_t n) { return ((n + 63u) & ~63u) + 64u; }
+__host__ __device__ constexpr size_t lx_words(uint32_t D, uint32_t E, uint32_t I)
+{
+    return LX_HEAD + 8ull * (lx_pad(E) + lx_pad(I) + lx_pad(D));
+}
+// true when k == 8 and the shape's grid fits on the device at once
+bool layer_supported(const MoeDims& d);
+// the whole MoE block of one token: hidden [D] += MoE(RMSNorm(hidden));
+// ids/w [K] receive the routing; err bit 0 reports an exchange time-out
+hipError_t launch_moe_layer(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx, uint32_t* ids,
+                            float* w, uint32_t* err, hipStream_t s);
 // out[slot * out_stride + row] = down_slot . h_slot   (per-expert outputs)
 hipError_t launch_down_slots(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n_exp,
                              const float* h, uint32_t h_stride, float* out,

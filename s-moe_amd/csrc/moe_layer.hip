@@ -1,0 +1,492 @@
+// moe_layer.hip -- batch-1 decode MoE block in one launch on gfx950.
+//
+// One top-k rank per XCD.  With k = 8 selected experts and the 8 XCDs of
+// MI355X, XCD x owns rank x: its waves stream expert ids[x]'s gate/up rows
+// and then its down rows, so the two exchanges inside the block stay in that
+// XCD's L2; only the final routing-weighted combine crosses XCDs.  Per wave
+// (block b, t = b / 8, on XCD x = XCC_ID; the dispatcher deals consecutive
+// blocks round-robin over the XCDs from some starting XCD, so t is unique
+// within an XCD):
+//   1. RMSNorm of the hidden state (common.hpp:245-256) and the bf16 router
+//      rows t, t + n, ... (common.hpp:293-306), published as flag-carrying
+//      words in XCD x's logit copy;
+//   2. softmax + top-k (scout.cpp:77-123) + renormalisation
+//      (decode.cpp:296-302) from that copy, in every wave;
+//   3. t < n_up: 8 rows of gate and up of expert ids[x] and
+//      h = silu(gate) * up (kernels.metal:240-337), published in XCD x's
+//      h copy;
+//   4. t < n_down: RW rows of expert ids[x]'s down matrix (kernels.metal:
+//      340-365) against all of h, staged in LDS; lane group g, lane c owns
+//      column chunk c of DR rows; the row totals go out as flag-carrying
+//      words through memory to the other XCDs;
+//   5. the wave of row block t on XCD t % 8 collects the k partial rows and
+//      writes hidden[row] += sum_r w_r * y_r[row] in rank order
+//      (decode.cpp:482-509).
+// The flag of every exchange word is the launch's tag, read from the epoch
+// word at the start; the combiner of row block 0 on XCD 0 advances the
+// epoch at its end.  Every wave produces a router row or a gate/up row block
+// (host-checked), and that combiner depends on all of them, so every wave has
+// read the tag before it changes; words never need re-arming, which keeps a
+// captured graph replayable.  All polls are bounded and report a timeout in
+// err bit 0.  The whole grid must be resident at once: the host checks it
+// against the occupancy of the kernel.
+#include <algorithm>
+
+#include "device_common.hpp"
+#include "kernels.hpp"
+#include "topk.hpp"
+
+namespace smoe {
+
+namespace {
+
+constexpr uint32_t LX_SPIN_LIMIT = 1u << 22;
+constexpr int LX_UP_RB = 8;     // gate/up rows per wave
+constexpr int LX_GROUP = 64;    // SMOE-Q4 group size (shatter_moe.py Q2_GROUP_SIZE)
+
+__device__ __forceinline__ uint64_t lx_word(float v, uint32_t tag)
+{
+    return (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v);
+}
+
+__device__ __forceinline__ uint32_t xcc_id()
+{
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(x));
+    return x & 7u;
+}
+
+// a store that only this XCD's waves read: it stays in this XCD's L2
+__device__ __forceinline__ void put_local(uint64_t* p, uint64_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+__device__ __forceinline__ void put_agent(uint64_t* p, uint64_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t get_agent(const uint64_t* p)
+{
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+template <int CPL, int VPL, int SEG, int DR>
+__global__ __launch_bounds__(WAVE)
+void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* __restrict__ lx,
+                 uint32_t* __restrict__ ids_out, float* __restrict__ w_out, uint32_t n_up, uint32_t n_down,
+                 uint32_t* __restrict__ err)
+{
+    constexpr int RB = LX_UP_RB;
+    constexpr int GL = 1 << SEG;       // lanes of one down group
+    constexpr int NG = WAVE / GL;      // down groups per wave
+    constexpr int RW = NG * DR;        // down rows per wave
+    constexpr int SH = SEG - ilog2(DR);
+    const int lane = threadIdx.x;
+    const uint32_t D = d.D, nch = D >> 5;
+    const uint32_t nbx = gridDim.x >> 3;
+    const uint32_t t = blockIdx.x >> 3;
+    const uint32_t x = xcc_id();
+
+    uint32_t tag = static_cast<uint32_t>(get_agent(lx)) + 1u;
+    tag = __builtin_amdgcn_readfirstlane(tag ? tag : 1u);
+    uint64_t* logc = lx + LX_HEAD + x * lx_pad(d.E);
+    uint64_t* hxc = lx + LX_HEAD + 8u * lx_pad(d.E) + x * lx_pad(d.I);
+    uint64_t* py = lx + LX_HEAD + 8u * lx_pad(d.E) + 8u * lx_pad(d.I);
+    const uint32_t py_stride = lx_pad(D);
+    bool timed_out = false;
+
+    // 1. hidden, norm weight and router rows t, t + nbx
+    const bool producer = t < d.E;
+    const bool second = t + nbx < d.E;
+    float4 xv[CPL][8];
+    uint4 g[CPL][4], rw[CPL][4], rw2[CPL][4];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xv[j][q] = load_f4(hidden + c * 32 + q * 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) g[j][q] = load_u4(L.norm_w + c * 32 + q * 8);
+    }
+    if (producer) {
+        const uint16_t* wr = L.router_w + static_cast<size_t>(t) * D;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) rw[j][q] = load_u4(wr + c * 32 + q * 8);
+        }
+        if (second) {
+            const uint16_t* wr2 = L.router_w + static_cast<size_t>(t + nbx) * D;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) rw2[j][q] = load_u4(wr2 + c * 32 + q * 8);
+            }
+        }
+    }
+    // 2. RMS norm: normed = (x * inv) * w, inv = 1 / sqrt(ss / n + 1e-6)
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const bool ok = lane + WAVE * j < nch;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            if (!ok) xv[j][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+            ss = fmaf(xv[j][q].x, xv[j][q].x, ss);
+            ss = fmaf(xv[j][q].y, xv[j][q].y, ss);
+            ss = fmaf(xv[j][q].z, xv[j][q].z, ss);
+            ss = fmaf(xv[j][q].w, xv[j][q].w, ss);
+        }
+    }
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + 1e-6f);
+    float a[CPL][32];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const uint32_t g0 = (q & 1) ? g[j][q >> 1].z : g[j][q >> 1].x;
+            const uint32_t g1 = (q & 1) ? g[j][q >> 1].w : g[j][q >> 1].y;
+            a[j][4 * q + 0] = (xv[j][q].x * inv) * bf16_to_f32(g0 & 0xFFFFu);
+            a[j][4 * q + 1] = (xv[j][q].y * inv) * bf16_to_f32(g0 >> 16);
+            a[j][4 * q + 2] = (xv[j][q].z * inv) * bf16_to_f32(g1 & 0xFFFFu);
+            a[j][4 * q + 3] = (xv[j][q].w * inv) * bf16_to_f32(g1 >> 16);
+        }
+    }
+    auto row_dot = [&](const uint4 (&w)[CPL][4]) {
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t w4[4] = {w[j][q].x, w[j][q].y, w[j][q].z, w[j][q].w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    acc = fmaf(bf16_to_f32(w4[u] & 0xFFFFu), a[j][8 * q + 2 * u], acc);
+                    acc = fmaf(bf16_to_f32(w4[u] >> 16), a[j][8 * q + 2 * u + 1], acc);
+                }
+            }
+        }
+        return wave_sum(acc);
+    };
+    if (producer) {
+        const float l0 = row_dot(rw);
+        if (lane == 0) put_local(logc + t, lx_word(l0, tag));
+        if (second) {
+            const float l1 = row_dot(rw2);
+            if (lane == 0) put_local(logc + t + nbx, lx_word(l1, tag));
+            for (uint32_t row = t + 2 * nbx; row < d.E; row += nbx) {
+                const uint16_t* wr = L.router_w + static_cast<size_t>(row) * D;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) rw[j][q] = load_u4(wr + c * 32 + q * 8);
+                }
+                const float lr = row_dot(rw);
+                if (lane == 0) put_local(logc + row, lx_word(lr, tag));
+            }
+        }
+    }
+    // digit form of the normed chunk (overlaps the logit exchange)
+    Q4Act qa[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) q4_act_from_floats(a[j], qa[j]);
+
+    // 2. the E logits of this XCD's copy, then softmax + top-k
+    float v[VPL];
+    {
+        uint32_t spins = 0;
+        bool all;
+        do {
+            all = true;
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) {
+                const uint32_t pos = lane + WAVE * j;
+                const uint64_t w64 = get_agent(logc + min(pos, d.E - 1));
+                v[j] = __uint_as_float(static_cast<uint32_t>(w64));
+                all &= pos >= d.E || static_cast<uint32_t>(w64 >> 32) == tag;
+            }
+            all = __ballot(!all) == 0;
+            if (!all && ++spins > LX_SPIN_LIMIT) {
+                timed_out = true;
+                break;
+            }
+        } while (!all);
+    }
+    uint32_t my_id;
+    float my_w;
+    __shared__ uint2 slots[TOPK_SLOTS];
+    topk_fast<VPL>(v, d.E, d.K, d.norm_topk, my_id, my_w, slots);
+    // (clamped: a timed-out exchange must still index inside the pool)
+    const uint32_t expert = min(readlane_u32(my_id, static_cast<int>(x)), d.E - 1);
+    if (x == 0 && t == 0 && static_cast<uint32_t>(lane) < d.K) {
+        ids_out[lane] = my_id;
+        w_out[lane] = my_w;
+    }
+    const uint8_t* blob = L.experts + static_cast<size_t>(expert) * L.stride;
+
+    // down rows of rank x: lane (group gi, chunk c) owns chunk c of rows
+    // rowb .. rowb + DR - 1
+    const uint32_t CH = d.I >> 5;
+    const int gi = lane >> SEG, c0 = lane & (GL - 1);
+    const bool act = static_cast<uint32_t>(c0) < CH;
+    const uint32_t dc = act ? static_cast<uint32_t>(c0) : CH - 1;
+    const uint32_t rowb = t * RW + gi * DR;
+    uint4 dv[DR];
+    uint16_t dsv[DR];
+    auto issue_down = [&] {
+        const uint8_t* pdn = blob + L.off[4];
+        const uint16_t* sdn = reinterpret_cast<const uint16_t*>(blob + L.off[5]);
+        const uint32_t drow_bytes = d.I >> 1, drow_scales = d.I / LX_GROUP;
+#pragma unroll
+        for (int i = 0; i < DR; ++i) {
+            const size_t row = rowb + i;
+            dv[i] = load_stream_u4(pdn + row * drow_bytes + dc * 16);
+            dsv[i] = load_stream_u16(sdn + row * drow_scales + (dc * 32) / LX_GROUP);
+        }
+    };
+
+    // 3. gate/up rows 8t .. 8t + 7 of rank x -> h.  (Issuing the down loads
+    //    any earlier than after this wave's up compute slows the launch:
+    //    they compete with the gate/up stream every wave waits for.)
+    if (t < n_up) {
+        const uint32_t rowg = t * RB;
+        const uint8_t* pa = blob + L.off[0];
+        const uint16_t* sa = reinterpret_cast<const uint16_t*>(blob + L.off[1]);
+        const uint8_t* pb = blob + L.off[2];
+        const uint16_t* sb = reinterpret_cast<const uint16_t*>(blob + L.off[3]);
+        const uint32_t row_bytes = D >> 1, row_scales = D / LX_GROUP;
+        uint4 va[RB][CPL], vb[RB][CPL];
+        uint16_t sva[RB][CPL], svb[RB][CPL];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            const size_t row = rowg + i;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const uint32_t c = min(lane + WAVE * j, nch - 1);
+                va[i][j] = load_stream_u4(pa + row * row_bytes + c * 16);
+                vb[i][j] = load_stream_u4(pb + row * row_bytes + c * 16);
+                sva[i][j] = load_stream_u16(sa + row * row_scales + (c * 32) / LX_GROUP);
+                svb[i][j] = load_stream_u16(sb + row * row_scales + (c * 32) / LX_GROUP);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float part[2 * RB];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            float ga = 0.f, ua = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                ga = fmaf(f16_bits_to_f32(sva[i][j]), q4_chunk_dot8(va[i][j], qa[j]), ga);
+                ua = fmaf(f16_bits_to_f32(svb[i][j]), q4_chunk_dot8(vb[i][j], qa[j]), ua);
+            }
+            part[2 * i] = ga;
+            part[2 * i + 1] = ua;
+        }
+        constexpr int USH = 6 - ilog2(2 * RB);
+        const float tot = wave_sum_rows<2 * RB>(part);
+        const float gv = __shfl(tot, (2 * lane) << USH);
+        const float uv = __shfl(tot, (2 * lane + 1) << USH);
+        // silu(z) = z * (1 / (1 + exp(-z)))  (kernels.metal:61-63, :334-336)
+        if (lane < RB) put_local(hxc + rowg + lane, lx_word((gv * (1.0f / (1.0f + expf(-gv)))) * uv, tag));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // 4. down rows of rank x against all of h
+    if (t < n_down) {
+        issue_down();
+        // all of this XCD's h, staged in LDS: passes of 16 words per lane,
+        // every load of a pass in flight before any is checked (addresses
+        // past the end re-read word I - 1)
+        __shared__ __align__(16) float h_s[LX_MAX_I];
+        {
+            const uint32_t passes = (d.I + 16 * WAVE - 1) / (16 * WAVE);
+            uint32_t spins = 0;
+            bool all;
+            do {
+                all = true;
+                for (uint32_t p = 0; p < passes; ++p) {
+                    uint64_t w64[16];
+#pragma unroll
+                    for (int m = 0; m < 16; ++m)
+                        w64[m] = get_agent(hxc + min(p * 16 * WAVE + lane + WAVE * m, d.I - 1));
+#pragma unroll
+                    for (int m = 0; m < 16; ++m) {
+                        h_s[min(p * 16 * WAVE + lane + WAVE * m, d.I - 1)] =
+                            __uint_as_float(static_cast<uint32_t>(w64[m]));
+                        all &= static_cast<uint32_t>(w64[m] >> 32) == tag;
+                    }
+                }
+                all = __ballot(!all) == 0;
+                if (!all) {
+                    if (++spins > LX_SPIN_LIMIT) {
+                        timed_out = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            } while (!all);
+        }
+        __builtin_amdgcn_wave_barrier();
+        float hx[32];
+        {
+            const float4* hp = reinterpret_cast<const float4*>(h_s + dc * 32);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const float4 f = hp[q];
+                hx[4 * q + 0] = f.x;
+                hx[4 * q + 1] = f.y;
+                hx[4 * q + 2] = f.z;
+                hx[4 * q + 3] = f.w;
+            }
+        }
+        Q4Act qh;
+        q4_act_from_floats(hx, qh);
+        float acc[DR];
+#pragma unroll
+        for (int i = 0; i < DR; ++i) {
+            const float y = f16_bits_to_f32(dsv[i]) * q4_chunk_dot8(dv[i], qh);
+            acc[i] = act ? y : 0.f;
+        }
+        // lane l holds the total of row (l >> SH) & (DR - 1) of group l >> SEG
+        const float tot = seg_sum_rows<DR, SEG>(acc);
+        const bool holder = (lane & ((1 << SH) - 1)) == 0;
+        const uint32_t myrow = t * RW + (lane >> SEG) * DR + ((lane >> SH) & (DR - 1));
+        if (holder) put_agent(py + x * py_stride + myrow, lx_word(tot, tag));
+
+        // 5. combine of row block t on XCD t % 8, in rank order
+        if ((t & 7u) == x) {
+            const int src = ((lane / DR) << SEG) | ((lane % DR) << SH);   // holder of row t*RW + lane
+            const float own = __shfl(tot, src & (WAVE - 1));
+            if (lane < RW) {
+                const uint32_t row = t * RW + lane;
+                float y[8];
+                uint32_t spins = 0;
+                bool all;
+                do {
+                    all = true;
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) {
+                        // the own rank's word is read too (branch-free) and ignored
+                        const uint64_t w64 = get_agent(py + r * py_stride + row);
+                        const bool mine = static_cast<uint32_t>(r) == x;
+                        y[r] = mine ? own : __uint_as_float(static_cast<uint32_t>(w64));
+                        all &= mine || static_cast<uint32_t>(w64 >> 32) == tag;
+                    }
+                    if (!all && ++spins > LX_SPIN_LIMIT) {
+                        timed_out = true;
+                        break;
+                    }
+                } while (!all);
+                float sum = 0.f;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) sum = fmaf(readlane_f32(my_w, r), y[r], sum);
+                hidden[row] = hidden[row] + sum;
+            }
+            if (x == 0 && t == 0) {
+                __builtin_amdgcn_wave_barrier();
+                if (lane == 0) put_agent(lx, static_cast<uint64_t>(tag));
+            }
+        }
+    }
+    if (timed_out) atomicOr(err, 1u);
+}
+
+namespace {
+
+struct LayerCfg {
+    int cpl, vpl, seg, dr;
+    uint32_t n_up, n_down, nbx;
+};
+
+template <int CPL, int VPL, int SEG, int DR>
+uint32_t resident_blocks()
+{
+    static uint32_t cap = [] {
+        int dev = 0, per_cu = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return 0u;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0u;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_layer<CPL, VPL, SEG, DR>, WAVE, 0) !=
+            hipSuccess)
+            return 0u;
+        return static_cast<uint32_t>(per_cu) * static_cast<uint32_t>(cus);
+    }();
+    return cap;
+}
+
+bool layer_cfg(const MoeDims& d, LayerCfg& c)
+{
+    if (d.K != 8 || d.group != 64 || d.E == 0 || d.E > SMOE_TOPK_MAX_N) return false;
+    if (d.D % 64 || d.I % 64 || d.I > LX_MAX_I) return false;
+    const uint32_t nch = d.D / 32;
+    c.cpl = nch <= 64 ? 1 : nch <= 128 ? 2 : 0;
+    if (!c.cpl) return false;
+    c.vpl = d.E <= 128 ? 2 : 8;
+    const uint32_t ch = d.I / 32;
+    if (ch <= 32) {
+        c.seg = 5;
+        c.dr = 8;
+    } else {
+        c.seg = 6;
+        c.dr = 32;
+    }
+    const uint32_t rw = (64u >> c.seg) * c.dr;
+    if (d.D % rw) return false;
+    c.n_up = d.I / LX_UP_RB;
+    c.n_down = d.D / rw;
+    c.nbx = std::max(c.n_up, c.n_down);
+    // every wave produces a router row or a gate/up row block
+    if (c.nbx > std::max(d.E, c.n_up)) return false;
+    return true;
+}
+
+template <int CPL, int VPL, int SEG, int DR>
+hipError_t launch_cfg(const LayerCfg& c, const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx,
+                      uint32_t* ids, float* w, uint32_t* err, hipStream_t s, bool dry)
+{
+    if (8u * c.nbx > resident_blocks<CPL, VPL, SEG, DR>()) return hipErrorInvalidConfiguration;
+    if (dry) return hipSuccess;
+    launch_kernel(k_moe_layer<CPL, VPL, SEG, DR>, dim3(8u * c.nbx), dim3(WAVE), s, d, L, hidden, lx, ids, w, c.n_up,
+                  c.n_down, err);
+    return hipGetLastError();
+}
+
+hipError_t dispatch(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx, uint32_t* ids, float* w,
+                    uint32_t* err, hipStream_t s, bool dry)
+{
+    LayerCfg c;
+    if (!layer_cfg(d, c)) return hipErrorInvalidValue;
+#define SMOE_LAYER_CASE(C, V, S, R)                                                           \
+    if (c.cpl == C && c.vpl == V && c.seg == S && c.dr == R)                                  \
+        return launch_cfg<C, V, S, R>(c, d, L, hidden, lx, ids, w, err, s, dry);
+    SMOE_LAYER_CASE(1, 2, 5, 8)
+    SMOE_LAYER_CASE(1, 2, 6, 32)
+    SMOE_LAYER_CASE(1, 8, 5, 8)
+    SMOE_LAYER_CASE(1, 8, 6, 32)
+    SMOE_LAYER_CASE(2, 2, 5, 8)
+    SMOE_LAYER_CASE(2, 2, 6, 32)
+    SMOE_LAYER_CASE(2, 8, 5, 8)
+    SMOE_LAYER_CASE(2, 8, 6, 32)
+#undef SMOE_LAYER_CASE
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool layer_supported(const MoeDims& d)
+{
+    return dispatch(d, LayerDesc{}, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, true) == hipSuccess;
+}
+
+hipError_t launch_moe_layer(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx, uint32_t* ids,
+                            float* w, uint32_t* err, hipStream_t s)
+{
+    return dispatch(d, L, hidden, lx, ids, w, err, s, false);
+}
+
+}  // namespace smoe

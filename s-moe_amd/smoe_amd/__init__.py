@@ -98,11 +98,11 @@ SIGNATURES = [
 
 KERNEL_MOE_UP, KERNEL_GATE_UP, KERNEL_MOE_DOWN, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
 KERNEL_PERMUTE, KERNEL_GROUPED_GATE_UP, KERNEL_GROUPED_DOWN, KERNEL_SCATTER = 5, 6, 7, 8
-KERNEL_ROUTE, KERNEL_SPLIT, KERNEL_STACK = 9, 10, 11
-DECODE_LAUNCHES, DECODE_PERSISTENT = 0, 1
+KERNEL_ROUTE, KERNEL_SPLIT, KERNEL_STACK, KERNEL_MOE_LAYER = 9, 10, 11, 12
+DECODE_LAUNCHES, DECODE_PERSISTENT, DECODE_SPLIT = 0, 1, 2
 KERNEL_NAMES = {0: "moe_up", 1: "gate_up", 2: "moe_down", 3: "down_slots", 4: "topk",
                 5: "permute", 6: "grouped_gate_up", 7: "grouped_down", 8: "combine", 9: "route",
-                10: "split", 11: "decode_stack"}
+                10: "split", 11: "decode_stack", 12: "moe_layer"}
 
 _lib = None
 
@@ -192,7 +192,8 @@ class Context:
                                                  n_tokens, ids or None, weights or None), "moe_decode")
 
     def set_decode_engine(self, engine: int):
-        """DECODE_LAUNCHES (two launches per layer) or DECODE_PERSISTENT (one launch per step)."""
+        """DECODE_LAUNCHES (per-layer calls), DECODE_PERSISTENT (one launch per step) or
+        DECODE_SPLIT (per-layer calls, always two launches per layer)."""
         self._check(self.lib.smoe_hip_set_decode_engine(self.ptr, engine), "set_decode_engine")
 
     def moe_decode_stack(self, shape, layers, hidden: int, ids: int = 0, weights: int = 0):

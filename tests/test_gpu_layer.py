@@ -1,0 +1,145 @@
+"""The one-launch decode block (k_moe_layer: one top-k rank per XCD) against
+the CPU oracle of decode.cpp:236-509, and against the two-launch form of the
+same block (SMOE_DECODE_SPLIT).  Top-k ids must be bit-exact; the MoE delta
+and the post-residual hidden state within 1e-3 per element (rel_err metric).
+The exchange words carry a per-launch tag and are never re-armed, so calls in
+a row and graph replays must reproduce the first result bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+import smoe_amd
+from gpu_helpers import Layer, hidden_states, moe_delta_err, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+# k = 8 shapes the one-launch kernel takes: Qwen3-30B-A3B, Qwen3-235B-A22B,
+# small ones (one router row per wave, E < waves per XCD, 512 experts)
+SHAPES = [
+    (2048, 128, 8, 768),
+    (4096, 128, 8, 1536),
+    (64, 8, 8, 64),
+    (256, 64, 8, 128),
+    (1024, 512, 8, 1024),
+    (512, 128, 8, 2048),
+]
+
+
+def layer_launches(ctx, fn):
+    """Run fn with dispatch profiling on; return the launch count of k_moe_layer
+    and of k_moe_up."""
+    ctx.profile_enable(True)
+    fn()
+    torch.cuda.synchronize()
+    n_layer, _ = ctx.profile_read(smoe_amd.KERNEL_MOE_LAYER)
+    n_up, _ = ctx.profile_read(smoe_amd.KERNEL_MOE_UP)
+    ctx.profile_enable(False)
+    return n_layer, n_up
+
+
+def decode(ctx, layer, hid):
+    ids = torch.zeros(layer.K, dtype=torch.int32, device="cuda")
+    w = torch.zeros(layer.K, dtype=torch.float32, device="cuda")
+    ctx.moe_decode(layer.shape, layer.layer, hid.data_ptr(), 1, ids.data_ptr(), w.data_ptr())
+    ctx.synchronize()
+    return ids.cpu().numpy().view(np.uint32), w.cpu().numpy()
+
+
+@pytest.mark.parametrize("D,E,K,I", SHAPES)
+def test_layer_vs_oracle(ctx, oracle, D, E, K, I):
+    layer = Layer(ctx, D, E, K, I, layer_id=D + E + I)
+    for index0 in (0, 9):
+        hid = hidden_states(ctx, 1, D, index0)[0]
+        h0 = hid.cpu().numpy()
+        n_layer, n_up = layer_launches(ctx, lambda: decode(ctx, layer, hid))
+        assert n_layer == 1 and n_up == 0, (n_layer, n_up)
+        gids, gw = decode(ctx, layer, hid.copy_(torch.from_numpy(h0).cuda()))
+        out, oid, ow, logits, normed, yo = layer.oracle_decode(oracle, h0)
+        assert (gids == oid).all(), (gids, oid)
+        assert np.allclose(gw, ow, rtol=1e-5, atol=1e-7)
+        got = hid.cpu().numpy()
+        e1, _ = moe_delta_err(got, h0, yo, ow)
+        e2, _ = rel_err(got, out)
+        print(f"{D}x{E}x{K}x{I} rel_err delta={e1:.2e} hidden={e2:.2e}")
+        assert max(e1, e2) <= TOL
+
+
+@pytest.mark.parametrize("D,E,K,I", [SHAPES[0], SHAPES[1]])
+def test_layer_matches_split_form(ctx, D, E, K, I):
+    """Same ids and weights as the two-launch form; hidden states within the
+    tolerance of each other (only the fp32 summation order differs)."""
+    layer = Layer(ctx, D, E, K, I, layer_id=5, host=False)
+    x0 = hidden_states(ctx, 1, D, 21)[0]
+    a = x0.clone()
+    ia, wa = decode(ctx, layer, a)
+    b = x0.clone()
+    ctx.set_decode_engine(smoe_amd.DECODE_SPLIT)
+    try:
+        n_layer, n_up = layer_launches(ctx, lambda: decode(ctx, layer, b))
+        assert n_layer == 0 and n_up == 1
+        b.copy_(x0)
+        ib, wb = decode(ctx, layer, b)
+    finally:
+        ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
+    assert (ia == ib).all() and np.array_equal(wa, wb)
+    x = x0.cpu().numpy().astype(np.float64)
+    da, db = a.cpu().numpy() - x, b.cpu().numpy() - x
+    slack = np.spacing(np.abs(a.cpu().numpy())) + np.spacing(np.abs(b.cpu().numpy()))
+    assert rel_err(da, db, slack=slack)[0] <= 2 * TOL
+
+
+def test_layer_calls_in_a_row_and_graph_replay(ctx):
+    """Many calls in a row (the tag advances every launch) and replays of a
+    captured 3-layer graph, with eager calls in between, all reproduce the
+    first result exactly."""
+    layers = [Layer(ctx, 2048, 128, 8, 768, layer_id=60 + i, host=False) for i in range(3)]
+    x0 = hidden_states(ctx, 1, 2048, 31)[0]
+
+    def run(buf):
+        for l in layers:
+            ctx.moe_decode(l.shape, l.layer, buf.data_ptr(), 1)
+
+    ref = x0.clone()
+    run(ref)
+    ctx.synchronize()
+    for _ in range(40):
+        buf = x0.clone()
+        run(buf)
+        ctx.synchronize()
+        assert torch.equal(buf, ref)
+    buf = x0.clone()
+    s = torch.cuda.Stream()
+    ctx.reserve(layers[0].shape, 1)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        ctx.set_stream(s.cuda_stream)
+        with torch.cuda.graph(g, stream=s):
+            run(buf)
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    for _ in range(5):
+        buf.copy_(x0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(buf, ref)
+        junk = x0.clone()
+        run(junk)
+        ctx.synchronize()
+        assert torch.equal(junk, ref)
+
+
+def test_shapes_outside_the_kernel_take_two_launches(ctx, oracle):
+    """k != 8 and batches of several tokens run the two-launch form."""
+    layer = Layer(ctx, 512, 128, 6, 256, layer_id=11)
+    hid = hidden_states(ctx, 1, 512, 4)[0]
+    n_layer, n_up = layer_launches(ctx, lambda: decode(ctx, layer, hid))
+    assert n_layer == 0 and n_up == 1
+    l8 = Layer(ctx, 256, 64, 8, 128, layer_id=12, host=False)
+    hid2 = hidden_states(ctx, 2, 256, 4)
+
+    def two_tokens():
+        ctx.moe_decode(l8.shape, l8.layer, hid2.data_ptr(), 2)
+    n_layer, n_up = layer_launches(ctx, two_tokens)
+    assert n_layer == 0 and n_up == 1
