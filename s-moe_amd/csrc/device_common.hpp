@@ -251,6 +251,21 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
     return readlane_u32(v, 63);
 }
 
+// Maximum over the 64 lanes, left in every lane (no readlane): rows by DPP,
+// then rows and halves by v_permlane16_swap / v_permlane32_swap, each of
+// which hands both sides of the exchange to every lane.
+__device__ __forceinline__ uint32_t wave_max_u32_all(uint32_t v)
+{
+    v = max(v, dpp_u32<DPP_QUAD_XOR1>(0u, v));
+    v = max(v, dpp_u32<DPP_QUAD_XOR2>(0u, v));
+    v = max(v, dpp_u32<DPP_ROW_ROR4>(0u, v));
+    v = max(v, dpp_u32<DPP_ROW_ROR8>(0u, v));
+    const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max(a[0], a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max(b[0], b[1]);
+}
+
 // ---- SMOE-Q4 16-byte chunk (32 codes, low nibble = even column) -----------
 // Returns sum_j code_j * x_j over the 32 columns of the chunk; x holds the
 // chunk's 32 activations.  Codes become floats exactly (0..15).

@@ -150,7 +150,7 @@ __device__ uint32_t topk_fast(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t 
             uint32_t lk = rem[0];
 #pragma unroll
             for (int j = 1; j < VPL; ++j) lk = max(lk, rem[j]);
-            const uint32_t K = wave_max_u32(lk);
+            const uint32_t K = wave_max_u32_all(lk);
 #pragma unroll
             for (int j = 0; j < VPL; ++j) {
                 const bool hit = rem[j] == K;
