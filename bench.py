@@ -84,10 +84,11 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="30b", choices=sorted(CONFIGS))
-    ap.add_argument("--workload", default="decode", choices=("decode", "prefill", "batched"),
+    ap.add_argument("--workload", default="decode", choices=("decode", "prefill", "batched", "vault"),
                     help="decode: the 48/94-layer batch-1 stack (default); prefill: 512 tokens through one "
                          "30B layer (configs[3]); batched: 64 tokens through one 235B layer with a Zipf "
-                         "router (configs[4])")
+                         "router (configs[4]); vault: .smoe vault -> HBM pool load rate (--layers layers "
+                         "of the --config shape, default 4)")
     ap.add_argument("--replicas", type=int, default=4, help="prefill/batched: layer replicas rotated")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (0: config's)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
@@ -116,6 +117,9 @@ def main():
 
     import smoe_amd
 
+    if args.workload == "vault":
+        vault_bench(args)
+        return
     if args.workload != "decode":
         grouped_bench(args)
         return
@@ -365,6 +369,68 @@ def zipf_router(torch, ctx, smoe_amd, router, u, D, E, layer, s_exp):
     w = router.view(torch.bfloat16).float().view(E, D).double().cpu()
     w = w + b[:, None] * u.double().cpu()[None, :]
     router.copy_(w.float().to(torch.bfloat16).view(torch.int16).view(-1).cuda())
+
+
+def vault_bench(args):
+    """Load rate of smoe_hip_vault_load: a vault of --layers synthetic layers
+    (the --config expert shape, all E experts) is written to a temporary file
+    from a pool generated on the GPU, then opened (every descriptor checked)
+    and copied into a fresh device pool, timed; the loaded pool must equal the
+    source bit for bit.  The file is read back from the page cache (dropping
+    it needs root), so the rate is host memory -> pinned staging -> PCIe ->
+    HBM, not disk."""
+    import tempfile
+
+    import torch
+
+    import smoe_amd
+    from smoe_amd import vault as V
+
+    c = CONFIGS[args.config]
+    D, E, K, I = c["D"], c["E"], c["K"], c["I"]
+    NL = args.layers or 4
+    dev = torch.device("cuda", 0)
+    ctx = smoe_amd.Context()
+    shape = smoe_amd.make_shape(D, E, K, I)
+    off, raw, stride = smoe_amd.blob_layout(D, I)
+    src = torch.empty(NL * E * stride, dtype=torch.uint8, device=dev)
+    ctx.synth_expert_pool(src.data_ptr(), 0, NL, E, stride, shape, SEED, 0.02)
+    host = src.cpu().numpy()
+    tmpdir = os.environ.get("TMPDIR", "/tmp")
+    with tempfile.NamedTemporaryFile(suffix=".smoe", dir=tmpdir) as tf:
+        t0 = time.perf_counter()
+        V.write_vault(tf.name, list(range(NL)), E, D, I,
+                      lambda l, e: host[(l * E + e) * stride:(l * E + e) * stride + raw].tobytes())
+        log(f"vault: wrote {NL} layers x {E} experts ({os.path.getsize(tf.name) / 1e9:.2f} GB) "
+            f"in {time.perf_counter() - t0:.1f} s")
+        del host
+        dst = torch.empty_like(src)
+        v = smoe_amd.Vault(tf.name)
+        v.load(dst.data_ptr(), dst.numel())                # warm: page cache and pinned allocation
+        times = []
+        for _ in range(max(1, min(args.steps, 5))):
+            dst.zero_()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            v2 = smoe_amd.Vault(tf.name)
+            v2.load(dst.data_ptr(), dst.numel())
+            times.append(time.perf_counter() - t0)
+            v2.close()
+        v.close()
+        same = bool(torch.equal(dst, src))
+    best = min(times)
+    line = {
+        "metric": "vault -> HBM expert pool load rate", "value": round(dst.numel() / best / 1e9, 2),
+        "unit": "GB/s", "n_gpus": 1, "steps": len(times), "higher_is_better": True,
+        "ms_per_load": round(best * 1e3, 2), "bytes": dst.numel(), "bit_exact": same,
+        "source": "page cache (file written just before)", "data": "synthetic SMOE-Q4 layers",
+        "config": {"workload": c["workload"] + "-vault-load", "layers": NL, "n_experts": E, "d_model": D,
+                   "d_ff": I},
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+    if not same:
+        sys.exit(1)
 
 
 def grouped_bench(args):

@@ -41,6 +41,7 @@ extern "C" {
 #define SMOE_ERR_HIP      -4   /* a HIP runtime call failed (see smoe_hip_last_error) */
 #define SMOE_ERR_CAPACITY -5   /* scratch reserved by smoe_hip_reserve is too small */
 #define SMOE_ERR_CAPTURE  -6   /* would allocate while the stream is being captured */
+#define SMOE_ERR_VAULT    -7   /* a .smoe vault is malformed or unreadable (smoe_hip_vault_error) */
 
 /* limits (reference: scout.hpp:32 MAX_ACTIVE, metal_bridge.h:134-135) */
 #define SMOE_MAX_ACTIVE        16
@@ -320,6 +321,51 @@ int smoe_hip_synth_expert_pool(SmoeMetalCtx* ctx, uint8_t* base, uint32_t first_
                                uint32_t n_layers, uint32_t n_experts,
                                uint64_t expert_stride, const SmoeMoeShape* shape,
                                uint64_t seed, float stddev);
+
+
+/* ---- .smoe vault -> HBM-resident expert pool ---------------------------
+ * Replaces the reference's expert streamer for this path
+ * (src/io/streamer.cpp parse_vault:183-212, main.cpp read_vault_header:96-157,
+ * read_expert_layout:167-198): the vault is parsed and checked once, every
+ * expert's table entry and three tensor descriptors against one common
+ * layout (the reference reads expert 0's descriptors only), and all blobs are
+ * copied into one device pool at pool + (m * E + e) * stride for the m-th MoE
+ * layer (ascending layer id) -- the layout smoe_hip_moe_decode and
+ * smoe_hip_moe_prefill take through SmoeMoeLayer.  Format: common.hpp:57-181.
+ * Host-side parsing needs no GPU; failures return SMOE_ERR_VAULT (or
+ * SMOE_ERR_BITS / SMOE_ERR_SHAPE / SMOE_ERR_ARG) and smoe_hip_vault_error()
+ * describes the last one of the calling thread. */
+typedef struct SmoeVault SmoeVault;
+
+typedef struct {
+    uint32_t version, num_moe_layers, experts_per_layer, total_experts;
+    uint32_t group_size, bits, d_model, d_ff, vocab_size, ffn_dim;
+    uint64_t blob_bytes;            /* raw bytes of one expert blob */
+    uint64_t stride;                /* page-padded blob size = pool stride */
+    uint64_t gate_packed_offset, gate_scales_offset;
+    uint64_t up_packed_offset,   up_scales_offset;
+    uint64_t down_packed_offset, down_scales_offset;
+    /* the v2 arch block (SmoeArchBlock, common.hpp:88-106) when arch_valid */
+    uint32_t arch_valid, arch_flags, num_heads, num_kv_heads, head_dim;
+    uint32_t moe_top_k, moe_ffn_dim, dense_ffn_dim, shared_expert_ffn_dim, num_hidden_layers;
+    float    rope_theta, rms_norm_eps;
+    char     model_type[24];
+} SmoeVaultInfo;
+
+int smoe_hip_vault_open(const char* path, SmoeVault** out);
+void smoe_hip_vault_close(SmoeVault* vault);
+int smoe_hip_vault_info(const SmoeVault* vault, SmoeVaultInfo* info);
+/* transformer layer id of the moe_index-th MoE layer */
+int smoe_hip_vault_layer_id(const SmoeVault* vault, uint32_t moe_index, uint32_t* layer_id);
+/* expert pointer, stride and blob offsets of MoE layer moe_index inside a pool
+ * loaded by smoe_hip_vault_load (norm_w and router_w are left as they are:
+ * they live in the Scout file, not in the vault) */
+int smoe_hip_vault_layer(const SmoeVault* vault, uint32_t moe_index, const void* dev_pool, SmoeMoeLayer* layer);
+/* copy every blob into dev_pool (>= num_moe_layers * experts_per_layer *
+ * stride bytes) through pinned staging, on hip_stream (NULL = null stream);
+ * returns when the copies are done */
+int smoe_hip_vault_load(const SmoeVault* vault, void* dev_pool, uint64_t pool_bytes, void* hip_stream);
+const char* smoe_hip_vault_error(void);
 
 /* ---- per-kernel timing (telemetry; cf. the reference's --instrument buckets,
  * decode.hpp:36-74, and smoe_metal_kernel_dispatches) ------------------------

@@ -20,6 +20,7 @@ SMOE_ERR_BITS = -3
 SMOE_ERR_HIP = -4
 SMOE_ERR_CAPACITY = -5
 SMOE_ERR_CAPTURE = -6
+SMOE_ERR_VAULT = -7
 _ERR_NAMES = {v: k for k, v in globals().items() if k.startswith("SMOE_ERR_")}
 
 SMOE_MAX_ACTIVE = 16
@@ -52,6 +53,18 @@ class SmoeMoeLayer(C.Structure):
                 ("expert_stride", C.c_uint64)] + [(n, C.c_uint64) for n in (
                     "gate_packed_offset", "gate_scales_offset", "up_packed_offset",
                     "up_scales_offset", "down_packed_offset", "down_scales_offset")]
+
+
+class SmoeVaultInfo(C.Structure):
+    _fields_ = ([(n, C.c_uint32) for n in ("version", "num_moe_layers", "experts_per_layer", "total_experts",
+                                           "group_size", "bits", "d_model", "d_ff", "vocab_size", "ffn_dim")]
+                + [(n, C.c_uint64) for n in ("blob_bytes", "stride", "gate_packed_offset", "gate_scales_offset",
+                                             "up_packed_offset", "up_scales_offset", "down_packed_offset",
+                                             "down_scales_offset")]
+                + [(n, C.c_uint32) for n in ("arch_valid", "arch_flags", "num_heads", "num_kv_heads", "head_dim",
+                                             "moe_top_k", "moe_ffn_dim", "dense_ffn_dim", "shared_expert_ffn_dim",
+                                             "num_hidden_layers")]
+                + [("rope_theta", C.c_float), ("rms_norm_eps", C.c_float), ("model_type", C.c_char * 24)])
 
 
 class SmoeExpertBlob(C.Structure):
@@ -91,6 +104,13 @@ SIGNATURES = [
     ("smoe_hip_synth_normal", _I, [_VP, _VP, _U64, _U64, _U64, _F]),
     ("smoe_hip_synth_bf16", _I, [_VP, _VP, _U64, _U64, _U64, _F]),
     ("smoe_hip_synth_expert_pool", _I, [_VP, _VP, _U32, _U32, _U32, _U64, _SHP, _U64, _F]),
+    ("smoe_hip_vault_open", _I, [C.c_char_p, C.POINTER(_VP)]),
+    ("smoe_hip_vault_close", None, [_VP]),
+    ("smoe_hip_vault_info", _I, [_VP, C.POINTER(SmoeVaultInfo)]),
+    ("smoe_hip_vault_layer_id", _I, [_VP, _U32, C.POINTER(C.c_uint32)]),
+    ("smoe_hip_vault_layer", _I, [_VP, _U32, _VP, _LAY]),
+    ("smoe_hip_vault_load", _I, [_VP, _VP, _U64, _VP]),
+    ("smoe_hip_vault_error", C.c_char_p, []),
     ("smoe_hip_profile_enable", _I, [_VP, _I]),
     ("smoe_hip_profile_read", _I, [_VP, _U32, C.POINTER(C.c_uint64), C.POINTER(C.c_double)]),
     ("smoe_hip_last_error", C.c_char_p, [_VP]),
@@ -262,3 +282,52 @@ class Context:
 
     def dispatches(self) -> int:
         return int(self.lib.smoe_metal_kernel_dispatches(self.ptr))
+
+
+class Vault:
+    """A parsed and checked .smoe vault (smoe_hip_vault_open); raises
+    SmoeError with the library's message when the file is malformed."""
+
+    def __init__(self, path: str):
+        self.lib = lib()
+        self.ptr = C.c_void_p()
+        rc = self.lib.smoe_hip_vault_open(os.fsencode(path), C.byref(self.ptr))
+        if rc != SMOE_OK:
+            self.ptr = None
+            raise SmoeError(f"vault_open: {_ERR_NAMES.get(rc, rc)} {self.lib.smoe_hip_vault_error().decode()}",
+                            rc)
+        self.info = SmoeVaultInfo()
+        self._check(self.lib.smoe_hip_vault_info(self.ptr, C.byref(self.info)), "vault_info")
+
+    def _check(self, rc, what):
+        if rc != SMOE_OK:
+            raise SmoeError(f"{what}: {_ERR_NAMES.get(rc, rc)} {self.lib.smoe_hip_vault_error().decode()}", rc)
+
+    def close(self):
+        if self.ptr:
+            self.lib.smoe_hip_vault_close(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def pool_bytes(self) -> int:
+        return self.info.num_moe_layers * self.info.experts_per_layer * self.info.stride
+
+    def layer_id(self, moe_index: int) -> int:
+        out = C.c_uint32()
+        self._check(self.lib.smoe_hip_vault_layer_id(self.ptr, moe_index, C.byref(out)), "vault_layer_id")
+        return int(out.value)
+
+    def layer(self, moe_index: int, dev_pool: int, norm_w: int = 0, router_w: int = 0) -> SmoeMoeLayer:
+        L = SmoeMoeLayer()
+        L.norm_w, L.router_w = norm_w or None, router_w or None
+        self._check(self.lib.smoe_hip_vault_layer(self.ptr, moe_index, dev_pool, C.byref(L)), "vault_layer")
+        return L
+
+    def load(self, dev_pool: int, pool_bytes: int, stream: int | None = None):
+        self._check(self.lib.smoe_hip_vault_load(self.ptr, dev_pool, pool_bytes, stream or None), "vault_load")
