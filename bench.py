@@ -84,11 +84,12 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="30b", choices=sorted(CONFIGS))
-    ap.add_argument("--workload", default="decode", choices=("decode", "prefill", "batched", "vault"),
+    ap.add_argument("--workload", default="decode", choices=("decode", "prefill", "batched", "vault", "prefill_stack"),
                     help="decode: the 48/94-layer batch-1 stack (default); prefill: 512 tokens through one "
                          "30B layer (configs[3]); batched: 64 tokens through one 235B layer with a Zipf "
                          "router (configs[4]); vault: .smoe vault -> HBM pool load rate (--layers layers "
-                         "of the --config shape, default 4)")
+                         "of the --config shape, default 4); prefill_stack: a 512-token prompt through the "
+                         "whole --config MoE stack, whole prompt per layer vs the reference's 64-token chunks")
     ap.add_argument("--replicas", type=int, default=4, help="prefill/batched: layer replicas rotated")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (0: config's)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
@@ -119,6 +120,9 @@ def main():
 
     if args.workload == "vault":
         vault_bench(args)
+        return
+    if args.workload == "prefill_stack":
+        prefill_stack_bench(args)
         return
     if args.workload != "decode":
         grouped_bench(args)
@@ -369,6 +373,89 @@ def zipf_router(torch, ctx, smoe_amd, router, u, D, E, layer, s_exp):
     w = router.view(torch.bfloat16).float().view(E, D).double().cpu()
     w = w + b[:, None] * u.double().cpu()[None, :]
     router.copy_(w.float().to(torch.bfloat16).view(torch.int16).view(-1).cuda())
+
+
+def prefill_stack_bench(args):
+    """Tokens/s of a T=512 prompt through every MoE layer of the --config stack
+    (smoe_hip_moe_prefill_stack; attention is not part of this path), with the
+    whole prompt per layer and, as the reference walks it, in 64-token chunks
+    (prefill.hpp:33): the chunked order streams every touched expert once per
+    chunk instead of once per pass.  Same results either way (tokens are
+    independent inside the MoE block)."""
+    import torch
+
+    import smoe_amd
+
+    c = dict(CONFIGS[args.config])
+    if args.layers:
+        c["layers"] = args.layers
+    D, E, K, I, NL = c["D"], c["E"], c["K"], c["I"], c["layers"]
+    T, CH = 512, 64
+    dev = torch.device("cuda", 0)
+    ctx = smoe_amd.Context()
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    ctx.set_stream(stream.cuda_stream)
+    shape = smoe_amd.make_shape(D, E, K, I)
+    off, raw, stride = smoe_amd.blob_layout(D, I)
+    log(f"prefill_stack: generating {NL} layers x {E} experts ({NL * E * stride / 1e9:.1f} GB)")
+    pool = torch.empty(NL * E * stride, dtype=torch.uint8, device=dev)
+    for l0 in range(0, NL, 8):
+        n = min(8, NL - l0)
+        ctx.synth_expert_pool(pool.data_ptr() + l0 * E * stride, l0, n, E, stride, shape, SEED, 0.02)
+        torch.cuda.synchronize()
+    router = torch.empty((NL, E * D), dtype=torch.int16, device=dev)
+    for l in range(NL):
+        ctx.synth_bf16(router[l].data_ptr(), E * D, SEED, smoe_amd.router_stream(l), 0.02)
+    norm_w = torch.full((D,), 0x3F80, dtype=torch.int16, device=dev)
+    h0 = torch.empty((T, D), dtype=torch.float32, device=dev)
+    for t in range(T):
+        ctx.synth_normal(h0[t].data_ptr(), D, SEED, smoe_amd.hidden_stream(t), 1.0)
+    layers = (smoe_amd.SmoeMoeLayer * NL)(*[smoe_amd.make_layer(norm_w.data_ptr(), router[l].data_ptr(),
+                                                                pool.data_ptr() + l * E * stride, stride, off)
+                                           for l in range(NL)])
+    hidden = h0.clone()
+
+    def whole():
+        ctx.moe_prefill_stack(shape, layers, hidden.data_ptr(), T)
+
+    def chunked():
+        for t0 in range(0, T, CH):
+            ctx.moe_prefill_stack(shape, layers, hidden[t0:].data_ptr(), CH)
+
+    res = {}
+    outs = {}
+    for name, fn in (("whole", whole), ("chunk64", chunked)):
+        hidden.copy_(h0)
+        fn()                      # warm-up (and scratch)
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(max(1, min(args.steps, 5))):
+            hidden.copy_(h0)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        res[name] = min(ts)
+        outs[name] = hidden.clone()
+        log(f"prefill_stack {name}: {res[name] * 1e3:.2f} ms for {T} tokens x {NL} layers")
+    ctx.synchronize()
+    same = bool(torch.equal(outs["whole"], outs["chunk64"]))
+    line = {
+        "metric": "MoE prefill tok/s, whole prompt per layer", "value": round(T / res["whole"], 1),
+        "unit": "tok/s", "n_gpus": 1, "steps": max(1, min(args.steps, 5)), "higher_is_better": True,
+        "ms_per_prompt": round(res["whole"] * 1e3, 2), "us_per_layer": round(res["whole"] * 1e6 / NL, 1),
+        "chunk64": {"tok_s": round(T / res["chunk64"], 1), "ms_per_prompt": round(res["chunk64"] * 1e3, 2)},
+        "speedup_vs_chunk64": round(res["chunk64"] / res["whole"], 2), "chunked_equal_bitwise": same,
+        "dtype": "f32 (f16 hi/lo MFMA operands)", "data": "synthetic",
+        "config": {"workload": c["workload"] + "-prefill-512", "layers": NL, "tokens": T, "chunk": CH,
+                   "d_model": D, "n_experts": E, "top_k": K, "d_ff": I},
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+    if not same:
+        sys.exit(1)
 
 
 def vault_bench(args):

@@ -281,6 +281,20 @@ int smoe_hip_moe_prefill(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
                          uint32_t* expert_offsets, uint32_t* sorted_tokens,
                          uint32_t* union_ids, uint32_t* union_size);
 
+
+/* The prefill layer loop (prefill.cpp:125-453, attention aside) over a stack
+ * of MoE layers, each over the whole prompt:
+ *   for l in 0 .. n_layers-1:  hidden [n_tokens x d_model] += MoE_l(RMSNorm_l(hidden))
+ * exactly n_layers smoe_hip_moe_prefill calls.  The reference walks the
+ * prompt in chunks of 64 tokens inside every layer (prefill.hpp:33); tokens
+ * are independent inside the MoE block, so a layer over all tokens gives the
+ * same results and streams each touched expert's weights once per pass of up
+ * to 736 tokens instead of once per chunk.  ids_out / weights_out
+ * [n_layers x n_tokens x top_k] are optional. */
+int smoe_hip_moe_prefill_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
+                               const SmoeMoeLayer* layers, uint32_t n_layers, float* hidden,
+                               uint32_t n_tokens, uint32_t* ids_out, float* weights_out);
+
 /* Scout::compute_top_k (scout.cpp:718-720 -> top_k :77-123) on device:
  * scores [n_rows x n] -> ids [n_rows x k], weights [n_rows x k]. */
 int smoe_hip_compute_top_k(SmoeMetalCtx* ctx, const float* scores, uint32_t n_rows,

@@ -839,6 +839,22 @@ extern "C" int smoe_hip_moe_prefill(SmoeMetalCtx* ctx, const SmoeMoeShape* shape
     return SMOE_OK;
 }
 
+extern "C" int smoe_hip_moe_prefill_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
+                                          const SmoeMoeLayer* layers, uint32_t n_layers, float* hidden,
+                                          uint32_t n_tokens, uint32_t* ids_out, float* weights_out)
+{
+    if (!ctx || !shape || !layers || !hidden || n_layers == 0 || n_tokens == 0) return SMOE_ERR_ARG;
+    const size_t per_layer = size_t(n_tokens) * shape->top_k;
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        const int rc = smoe_hip_moe_prefill(ctx, shape, &layers[l], hidden, n_tokens,
+                                            ids_out ? ids_out + l * per_layer : nullptr,
+                                            weights_out ? weights_out + l * per_layer : nullptr, nullptr, nullptr,
+                                            nullptr, nullptr);
+        if (rc != SMOE_OK) return rc;
+    }
+    return SMOE_OK;
+}
+
 extern "C" int smoe_hip_compute_top_k(SmoeMetalCtx* ctx, const float* scores, uint32_t n_rows, uint32_t n,
                                       uint32_t k, uint32_t* ids, float* weights, int norm_topk)
 {

@@ -98,6 +98,7 @@ SIGNATURES = [
     ("smoe_hip_moe_decode_stack", _I, [_VP, _SHP, _LAY, _U32, _VP, _VP, _VP]),
     ("smoe_hip_set_decode_engine", _I, [_VP, _I]),
     ("smoe_hip_moe_prefill", _I, [_VP, _SHP, _LAY, _VP, _U32, _VP, _VP, _VP, _VP, _VP, _VP]),
+    ("smoe_hip_moe_prefill_stack", _I, [_VP, _SHP, _LAY, _U32, _VP, _U32, _VP, _VP]),
     ("smoe_hip_compute_top_k", _I, [_VP, _VP, _U32, _U32, _U32, _VP, _VP, _I]),
     ("smoe_hip_permute", _I, [_VP, _VP, _VP, _U32, _U32, _U32, _VP, _VP, _VP, _VP, _VP]),
     ("smoe_hip_quantize_q4", _I, [_VP, _VP, _U64, _U32, _VP, _VP]),
@@ -210,6 +211,14 @@ class Context:
     def moe_decode(self, shape, layer, hidden: int, n_tokens: int, ids: int = 0, weights: int = 0):
         self._check(self.lib.smoe_hip_moe_decode(self.ptr, C.byref(shape), C.byref(layer), hidden,
                                                  n_tokens, ids or None, weights or None), "moe_decode")
+
+    def moe_prefill_stack(self, shape, layers, hidden: int, n_tokens: int, ids: int = 0, weights: int = 0):
+        """layers: a sequence of SmoeMoeLayer (or a ctypes array of them)."""
+        if not isinstance(layers, C.Array):
+            layers = (SmoeMoeLayer * len(layers))(*layers)
+        self._check(self.lib.smoe_hip_moe_prefill_stack(self.ptr, C.byref(shape), layers, len(layers), hidden,
+                                                        n_tokens, ids or None, weights or None),
+                    "moe_prefill_stack")
 
     def set_decode_engine(self, engine: int):
         """DECODE_LAUNCHES (per-layer calls), DECODE_PERSISTENT (one launch per step) or
