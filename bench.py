@@ -84,12 +84,13 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="30b", choices=sorted(CONFIGS))
-    ap.add_argument("--workload", default="decode", choices=("decode", "prefill", "batched", "vault", "prefill_stack"),
+    ap.add_argument("--workload", default="decode", choices=("decode", "prefill", "batched", "vault", "prefill_stack", "trunk"),
                     help="decode: the 48/94-layer batch-1 stack (default); prefill: 512 tokens through one "
                          "30B layer (configs[3]); batched: 64 tokens through one 235B layer with a Zipf "
                          "router (configs[4]); vault: .smoe vault -> HBM pool load rate (--layers layers "
                          "of the --config shape, default 4); prefill_stack: a 512-token prompt through the "
-                         "whole --config MoE stack, whole prompt per layer vs the reference's 64-token chunks")
+                         "whole --config MoE stack, whole prompt per layer vs the reference's 64-token chunks; trunk: the "
+                         "dense-trunk GEMV and decode attention layer (30B head layout)")
     ap.add_argument("--replicas", type=int, default=4, help="prefill/batched: layer replicas rotated")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (0: config's)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
@@ -123,6 +124,9 @@ def main():
         return
     if args.workload == "prefill_stack":
         prefill_stack_bench(args)
+        return
+    if args.workload == "trunk":
+        trunk_bench(args)
         return
     if args.workload != "decode":
         grouped_bench(args)
@@ -373,6 +377,88 @@ def zipf_router(torch, ctx, smoe_amd, router, u, D, E, layer, s_exp):
     w = router.view(torch.bfloat16).float().view(E, D).double().cpu()
     w = w + b[:, None] * u.double().cpu()[None, :]
     router.copy_(w.float().to(torch.bfloat16).view(torch.int16).view(-1).cuda())
+
+
+def trunk_bench(args):
+    """Dense trunk around the MoE block: GB/s of the bf16 GEMV (an o_proj-sized
+    and an lm_head-sized matrix) and time of one decode attention layer
+    (Qwen3-30B-A3B layout: 32 query / 4 KV heads of 128, d_model 2048) at
+    several context lengths.  Algorithmic bytes: the bf16 weights once, plus
+    for attention the K and V rows of the valid positions (fp32) and x/outputs.
+    Times from HIP events around --steps back-to-back calls on the stream."""
+    import torch
+
+    import smoe_amd
+
+    ctx = smoe_amd.Context()
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+    ctx.set_stream(stream.cuda_stream)
+    steps = max(4, args.steps if args.steps != 256 else 50)
+
+    def timed_us(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    out = {"gemv": {}, "attention": {}}
+    for name, (rows, cols) in (("o_proj_2048x4096", (2048, 4096)), ("lm_head_151936x2048", (151936, 2048))):
+        w = torch.empty(rows * cols, dtype=torch.int16, device="cuda")
+        ctx.synth_bf16(w.data_ptr(), rows * cols, SEED, 0xABC0 + rows, 0.02)
+        x = torch.randn(cols, device="cuda")
+        y = torch.empty(rows, device="cuda")
+        us = timed_us(lambda: ctx.matvec_bf16(w.data_ptr(), x.data_ptr(), y.data_ptr(), rows, cols))
+        b = rows * cols * 2 + cols * 4 + rows * 4
+        out["gemv"][name] = {"us": round(us, 2), "bytes": b, "gbs": round(b / us / 1e3, 1),
+                             "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 3)}
+        log(f"gemv {name}: {us:.2f} us, {b / us / 1e3:.0f} GB/s")
+        del w
+    d_model, nh, nkv, hd = 2048, 32, 4, 128
+    q_dim, kv_dim = nh * hd, nkv * hd
+    W = {}
+    for i, (n, (r, c)) in enumerate(dict(q=(q_dim, d_model), k=(kv_dim, d_model), v=(kv_dim, d_model),
+                                         o=(d_model, q_dim)).items()):
+        W[n] = torch.empty(r * c, dtype=torch.int16, device="cuda")
+        ctx.synth_bf16(W[n].data_ptr(), r * c, SEED, 0xABD0 + i, 0.02)
+    nw = torch.full((hd,), 0x3F80, dtype=torch.int16, device="cuda")
+    wbytes = sum(t.numel() * 2 for t in W.values())
+    for ctx_len in (1024, 4096, 32768):
+        kc = torch.randn(ctx_len, kv_dim, device="cuda")
+        vc = torch.randn(ctx_len, kv_dim, device="cuda")
+        buf = {n: torch.zeros(sz, device="cuda") for n, sz in (("x", d_model), ("q", q_dim), ("k", kv_dim),
+                                                                ("v", kv_dim), ("att", q_dim), ("o", d_model),
+                                                                ("cos", hd // 2), ("sin", hd // 2))}
+        buf["x"].normal_()
+        buf["cos"].fill_(1.0)
+        a = smoe_amd.SmoeAttnLayerArgs()
+        a.w_q, a.w_k, a.w_v, a.w_o = (W[n].data_ptr() for n in "qkvo")
+        a.q_norm_w = a.k_norm_w = nw.data_ptr()
+        a.rope_cos, a.rope_sin, a.normed_in = buf["cos"].data_ptr(), buf["sin"].data_ptr(), buf["x"].data_ptr()
+        a.qbuf, a.kbuf, a.vbuf = buf["q"].data_ptr(), buf["k"].data_ptr(), buf["v"].data_ptr()
+        a.k_cache, a.v_cache, a.attn_out, a.o_out = (kc.data_ptr(), vc.data_ptr(), buf["att"].data_ptr(),
+                                                     buf["o"].data_ptr())
+        a.d_model, a.q_dim, a.kv_dim, a.head_dim, a.num_heads, a.num_kv_heads = d_model, q_dim, kv_dim, hd, nh, nkv
+        a.slot, a.valid, a.attn_ctx, a.attn_scale = ctx_len - 1, ctx_len, ctx_len, 1.0 / hd ** 0.5
+        us = timed_us(lambda: ctx.attention_layer(a))
+        b = wbytes + 2 * ctx_len * kv_dim * 4 + (d_model + q_dim) * 4
+        out["attention"][f"ctx{ctx_len}"] = {"us": round(us, 2), "bytes": b, "gbs": round(b / us / 1e3, 1),
+                                              "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 3)}
+        log(f"attention ctx {ctx_len}: {us:.2f} us, {b / us / 1e3:.0f} GB/s")
+        del kc, vc
+    ctx.synchronize()
+    lm = out["gemv"]["lm_head_151936x2048"]
+    line = {"metric": "dense-trunk bf16 GEMV GB/s (lm_head-sized)", "value": lm["gbs"], "unit": "GB/s",
+            "n_gpus": 1, "steps": steps, "higher_is_better": True, "dtype": "bf16 weights, f32 accumulate",
+            "data": "synthetic", "config": {"workload": "qwen3-30b-a3b-dense-trunk", "head_layout": "32q/4kv x 128"},
+            **out}
+    print(json.dumps(line), flush=True)
+    ctx.close()
 
 
 def prefill_stack_bench(args):

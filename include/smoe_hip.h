@@ -147,9 +147,13 @@ void smoe_metal_scout_matvec_group_bf16(SmoeMetalCtx* ctx, const uint16_t** weig
                                         const uint32_t* rows, const uint32_t* cols,
                                         uint32_t count);
 
-/* metal_bridge.h:166-196 -- fused decode attention.  Attention is outside
- * this library's scope (the MoE block only): the symbol exists so the
- * reference callers link; it reports on stderr and leaves o_out untouched. */
+/* metal_bridge.h:166-196 -- fused decode attention of one token: QKV
+ * projections, per-head QK RMSNorm + RoPE + KV ring append, GQA attention over
+ * `valid` positions counted back from `slot`, O projection
+ * (decode.cpp:150-229; kernels.metal:421-652).  As on the reference, the call
+ * is synchronous: o_out is valid on return.  Every pointer is a device
+ * address (weights and the KV ring resident in HBM, like the experts); see
+ * smoe_hip_attention_layer for the asynchronous form. */
 typedef struct {
     const uint16_t* w_q;
     const uint16_t* w_k;
@@ -337,6 +341,25 @@ int smoe_hip_synth_expert_pool(SmoeMetalCtx* ctx, uint8_t* base, uint32_t first_
                                uint64_t seed, float stddev);
 
 
+/* ---- dense trunk, device-resident (MI355X path) ---------------------------
+ * y [rows] = W [rows x cols] bf16 . x [cols] fp32 (common.hpp:293-306), all
+ * device pointers, asynchronous on the context stream.  cols % 8 == 0,
+ * cols <= 16384, W and x 16-byte aligned.  The group form runs `count`
+ * independent products in one launch (host arrays of device pointers;
+ * metal_bridge.h:210-216). */
+int smoe_hip_matvec_bf16(SmoeMetalCtx* ctx, const uint16_t* w, const float* x, float* y,
+                         uint32_t rows, uint32_t cols);
+int smoe_hip_matvec_group_bf16(SmoeMetalCtx* ctx, const uint16_t* const* w, const float* const* x,
+                               float* const* y, const uint32_t* rows, const uint32_t* cols,
+                               uint32_t count);
+/* smoe_metal_attention_layer without the final synchronisation: the result
+ * lands in args->o_out in stream order.  head_dim a multiple of 64 up to 256,
+ * num_heads a multiple of num_kv_heads, q_dim = num_heads * head_dim,
+ * kv_dim = num_kv_heads * head_dim, slot < attn_ctx, 1 <= valid <= attn_ctx.
+ * q_norm_w / k_norm_w NULL skip the QK norm.  Scratch for the context splits
+ * grows outside graph capture (else SMOE_ERR_CAPTURE). */
+int smoe_hip_attention_layer(SmoeMetalCtx* ctx, const SmoeAttnLayerArgs* args);
+
 /* ---- .smoe vault -> HBM-resident expert pool ---------------------------
  * Replaces the reference's expert streamer for this path
  * (src/io/streamer.cpp parse_vault:183-212, main.cpp read_vault_header:96-157,
@@ -399,6 +422,8 @@ const char* smoe_hip_vault_error(void);
 #define SMOE_KERNEL_SPLIT        10   /* prefill: f16 hi/lo planes of activations             */
 #define SMOE_KERNEL_STACK        11   /* decode: every layer of a stack in one launch         */
 #define SMOE_KERNEL_MOE_LAYER    12   /* decode: the whole MoE block of one token in one launch */
+#define SMOE_KERNEL_GEMV         13   /* dense trunk: grouped bf16 GEMV                          */
+#define SMOE_KERNEL_ATTENTION    14   /* dense trunk: QK norm/RoPE/KV append + decode attention   */
 #define SMOE_KERNEL_KINDS        16
 int smoe_hip_profile_enable(SmoeMetalCtx* ctx, int enable);
 int smoe_hip_profile_read(SmoeMetalCtx* ctx, uint32_t kernel, uint64_t* launches, double* total_ms);

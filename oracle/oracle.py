@@ -86,6 +86,9 @@ def lib():
                                       C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
         L.orc_moe_decode_layer.argtypes = [C.POINTER(OrcShape), C.POINTER(OrcLayer), _f32p,
                                            _u32p, _f32p, C.c_void_p, C.c_void_p, C.c_void_p]
+        _u16n = C.c_void_p   # optional bf16 norm weights (None skips the norm)
+        L.orc_attention_layer.argtypes = [_u16p, _u16p, _u16p, _u16p, _u16n, _u16n, _f32p, _f32p, _f32p,
+                                          _f32p, _f32p, _f32p] + [C.c_uint32] * 7 + [C.c_float]
         L.orc_permute.restype = C.c_uint32
         L.orc_permute.argtypes = [_u32p, _f32p, C.c_uint32, C.c_uint32, C.c_uint32, _u32p,
                                   _u32p, _f32p, _u32p]
@@ -276,3 +279,24 @@ def permute(ids, w, n_experts):
     uni = np.zeros(n_experts, np.uint32)
     nu = lib().orc_permute(ids, w, T, K, n_experts, offsets, tok, wo, uni)
     return offsets, tok, wo, uni[:nu]
+
+
+def attention_layer(w_q, w_k, w_v, w_o, q_norm_w, k_norm_w, rope_cos, rope_sin, normed_in, k_cache, v_cache,
+                    head_dim, num_heads, num_kv_heads, slot, valid, scale):
+    """decode.cpp:150-229 (CPU branch).  Weights uint16 bf16 bits (norm weights
+    may be None); k_cache / v_cache [attn_ctx x kv_dim] are copied and the copies
+    updated.  Returns (o_out, k_cache, v_cache)."""
+    kc = np.array(k_cache, np.float32, copy=True)
+    vc = np.array(v_cache, np.float32, copy=True)
+    d_model = len(normed_in)
+    o = np.zeros(d_model, np.float32)
+    c16 = lambda a: np.ascontiguousarray(a, np.uint16)
+    qn = c16(q_norm_w) if q_norm_w is not None else None
+    kn = c16(k_norm_w) if k_norm_w is not None else None
+    lib().orc_attention_layer(c16(w_q), c16(w_k), c16(w_v), c16(w_o),
+                              qn.ctypes.data if qn is not None else None, kn.ctypes.data if kn is not None else None,
+                              np.ascontiguousarray(rope_cos, np.float32), np.ascontiguousarray(rope_sin, np.float32),
+                              np.ascontiguousarray(normed_in, np.float32), kc, vc, o, d_model, head_dim, num_heads,
+                              num_kv_heads, slot, valid, kc.shape[0], scale)
+    return o, kc, vc
+

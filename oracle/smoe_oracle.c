@@ -508,3 +508,77 @@ void orc_moe_prefill_layer(const OrcShape* s, const OrcLayer* L, float* hidden,
     }
     free(normed); free(routed); free(logits); free(h); free(y);
 }
+
+/* ------------------------------------------------------------------------ */
+/* F4: decode attention of one token (decode.cpp:150-229, the CPU branch)   */
+/* ------------------------------------------------------------------------ */
+void orc_attention_layer(const uint16_t* w_q, const uint16_t* w_k, const uint16_t* w_v, const uint16_t* w_o,
+                         const uint16_t* q_norm_w, const uint16_t* k_norm_w, const float* rope_cos,
+                         const float* rope_sin, const float* normed_in, float* k_cache, float* v_cache,
+                         float* o_out, uint32_t d_model, uint32_t head_dim, uint32_t num_heads,
+                         uint32_t num_kv_heads, uint32_t slot, uint32_t valid, uint32_t attn_ctx, float scale)
+{
+    const uint32_t q_dim = num_heads * head_dim, kv_dim = num_kv_heads * head_dim, half = head_dim / 2;
+    float* q = (float*)malloc(q_dim * sizeof(float));
+    float* k = (float*)malloc(kv_dim * sizeof(float));
+    float* v = (float*)malloc(kv_dim * sizeof(float));
+    float* att = (float*)calloc(q_dim, sizeof(float));
+    float* sc = (float*)malloc((size_t)valid * sizeof(float));
+    if (!q || !k || !v || !att || !sc) goto done;
+    orc_matvec_bf16(q, w_q, normed_in, q_dim, d_model);                 /* :151-153 */
+    orc_matvec_bf16(k, w_k, normed_in, kv_dim, d_model);
+    orc_matvec_bf16(v, w_v, normed_in, kv_dim, d_model);
+    if (q_norm_w)                                                        /* :156-165 */
+        for (uint32_t h = 0; h < num_heads; ++h) orc_rms_norm_bf16(q + h * head_dim, q_norm_w, head_dim);
+    if (k_norm_w)
+        for (uint32_t h = 0; h < num_kv_heads; ++h) orc_rms_norm_bf16(k + h * head_dim, k_norm_w, head_dim);
+    for (uint32_t h = 0; h < num_heads; ++h)                             /* :168-176 */
+        for (uint32_t d = 0; d < half; ++d) {
+            float* x = q + h * head_dim;
+            const float x0 = x[d], x1 = x[d + half];
+            x[d] = x0 * rope_cos[d] - x1 * rope_sin[d];
+            x[d + half] = x0 * rope_sin[d] + x1 * rope_cos[d];
+        }
+    for (uint32_t h = 0; h < num_kv_heads; ++h)                          /* :178-186 */
+        for (uint32_t d = 0; d < half; ++d) {
+            float* x = k + h * head_dim;
+            const float x0 = x[d], x1 = x[d + half];
+            x[d] = x0 * rope_cos[d] - x1 * rope_sin[d];
+            x[d + half] = x0 * rope_sin[d] + x1 * rope_cos[d];
+        }
+    memcpy(k_cache + (size_t)slot * kv_dim, k, kv_dim * sizeof(float)); /* :189-190 */
+    memcpy(v_cache + (size_t)slot * kv_dim, v, kv_dim * sizeof(float));
+    for (uint32_t h = 0; h < num_heads; ++h) {                           /* :193-226 */
+        const uint32_t kv_h = h / (num_heads / num_kv_heads);
+        const float* qh = q + h * head_dim;
+        for (uint32_t i = 0; i < valid; ++i) {
+            const uint32_t ki = (slot - i + attn_ctx) % attn_ctx;
+            const float* kr = k_cache + (size_t)ki * kv_dim + kv_h * head_dim;
+            float s = 0.0f;                                              /* dot_f32, common.hpp:339-344 */
+            for (uint32_t d = 0; d < head_dim; ++d) s += qh[d] * kr[d];
+            sc[i] = s * scale;
+        }
+        float m = sc[0];
+        for (uint32_t i = 1; i < valid; ++i)
+            if (sc[i] > m) m = sc[i];
+        float sum = 0.0f;
+        for (uint32_t i = 0; i < valid; ++i) {
+            sc[i] = expf(sc[i] - m);
+            sum += sc[i];
+        }
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        for (uint32_t i = 0; i < valid; ++i) sc[i] *= inv;
+        for (uint32_t i = 0; i < valid; ++i) {
+            const uint32_t vi = (slot - i + attn_ctx) % attn_ctx;
+            orc_axpy_f32(att + h * head_dim, sc[i], v_cache + (size_t)vi * kv_dim + kv_h * head_dim, head_dim);
+        }
+    }
+    orc_matvec_bf16(o_out, w_o, att, d_model, q_dim);                   /* :229 */
+done:
+    free(q);
+    free(k);
+    free(v);
+    free(att);
+    free(sc);
+}
+

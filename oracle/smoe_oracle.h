@@ -133,6 +133,22 @@ float    orc_union_w(uint32_t expert, uint32_t t);
 void orc_moe_prefill_layer(const OrcShape* s, const OrcLayer* L, float* hidden,
                            uint32_t T, uint32_t* ids, float* weights);
 
+/* ---- F4: decode attention of one token -----------------------------------
+ * decode.cpp:150-229 (CPU branch): QKV GEMVs, per-head QK RMSNorm (NULL norm
+ * weights skip it), RoPE on (d, d + head_dim/2), K and V written to the ring
+ * at slot, per head softmax over valid positions counted back from slot
+ * (sequential sums, expf), axpy of V rows, O GEMV into o_out [d_model].
+ * Pinned by its compiled-reference pieces (matvec_bf16, rms_norm_bf16,
+ * axpy_f32) and by closed forms in tests/test_oracle_attention.py: one
+ * position returns its V row, identical keys average V, RoPE at angle 0 is
+ * the identity and at 90 degrees maps (a, b) to (-b, a), a normed head has
+ * unit RMS. */
+void orc_attention_layer(const uint16_t* w_q, const uint16_t* w_k, const uint16_t* w_v, const uint16_t* w_o,
+                         const uint16_t* q_norm_w, const uint16_t* k_norm_w, const float* rope_cos,
+                         const float* rope_sin, const float* normed_in, float* k_cache, float* v_cache,
+                         float* o_out, uint32_t d_model, uint32_t head_dim, uint32_t num_heads,
+                         uint32_t num_kv_heads, uint32_t slot, uint32_t valid, uint32_t attn_ctx, float scale);
+
 #ifdef __cplusplus
 }
 #endif

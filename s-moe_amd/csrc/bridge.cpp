@@ -94,6 +94,8 @@ struct SmoeMetalCtx {
     uint32_t* d_err = nullptr;       // [1] device-side error flags (bit 0: exchange time-out, bit 1: bad expert id)
     uint32_t* perm_pairs = nullptr;  // smoe_hip_permute's sorted pair ids
     float* mv_in = nullptr;          // reference-surface GEMV staging
+    float* attn_part = nullptr;      // decode attention: per-(head, split) partials
+    size_t attn_part_cap = 0;
     float* mv_out = nullptr;
     uint32_t mv_cap = 0;
     uint64_t perm_cap = 0;
@@ -433,6 +435,7 @@ extern "C" void smoe_metal_destroy(SmoeMetalCtx* ctx)
     dfree(ctx->perm_pairs);
     dfree(ctx->mv_in);
     dfree(ctx->mv_out);
+    dfree(ctx->attn_part);
     dfree(ctx->d_err);
     dfree(ctx->d_input);
     dfree(ctx->d_hidden);
@@ -562,6 +565,24 @@ extern "C" void smoe_metal_register_buffer(SmoeMetalCtx* ctx, const void* ptr, s
 }
 
 // dense bf16 GEMVs of the reference surface: host vectors in and out
+// the grouped GEMV where its layout rules hold, else the plain one-wave-per-row kernel
+static hipError_t gemv_or_plain(const uint16_t* w, const float* x, float* y, uint32_t rows, uint32_t cols,
+                                hipStream_t st)
+{
+    if (cols % 8 == 0 && cols <= smoe::GEMV_MAX_COLS && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+        smoe::GemvGroup g{};
+        g.w[0] = w;
+        g.x[0] = x;
+        g.y[0] = y;
+        g.rows[0] = rows;
+        g.cols[0] = cols;
+        g.count = 1;
+        return smoe::launch_gemv_bf16(g, st);
+    }
+    return smoe::launch_matvec_bf16(w, x, y, rows, cols, st);
+}
+
 static bool matvec_one(SmoeMetalCtx* ctx, const uint16_t* w, const float* in, float* out, uint32_t rows,
                        uint32_t cols)
 {
@@ -576,7 +597,7 @@ static bool matvec_one(SmoeMetalCtx* ctx, const uint16_t* w, const float* in, fl
     }
     return hip_ok(ctx, hipMemcpyAsync(ctx->mv_in, in, size_t(cols) * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
                   "hipMemcpyAsync") &&
-           hip_ok(ctx, smoe::launch_matvec_bf16(w, ctx->mv_in, ctx->mv_out, rows, cols, ctx->stream), "matvec_bf16") &&
+           hip_ok(ctx, gemv_or_plain(w, ctx->mv_in, ctx->mv_out, rows, cols, ctx->stream), "matvec_bf16") &&
            hip_ok(ctx, hipMemcpyAsync(out, ctx->mv_out, size_t(rows) * sizeof(float), hipMemcpyDeviceToHost,
                                       ctx->stream),
                   "hipMemcpyAsync") &&
@@ -609,11 +630,82 @@ extern "C" void smoe_metal_scout_matvec_group_bf16(SmoeMetalCtx* ctx, const uint
     smoe_metal_scout_matvec_batch_bf16(ctx, weights, inputs, outputs, rows, cols, count);
 }
 
+extern "C" int smoe_hip_matvec_group_bf16(SmoeMetalCtx* ctx, const uint16_t* const* w, const float* const* x,
+                                          float* const* y, const uint32_t* rows, const uint32_t* cols, uint32_t count)
+{
+    if (!ctx || !w || !x || !y || !rows || !cols || count == 0) return SMOE_ERR_ARG;
+    for (uint32_t i0 = 0; i0 < count; i0 += smoe::GEMV_MAX) {
+        smoe::GemvGroup g{};
+        g.count = std::min<uint32_t>(smoe::GEMV_MAX, count - i0);
+        for (uint32_t j = 0; j < g.count; ++j) {
+            const uint32_t i = i0 + j;
+            if (!w[i] || !x[i] || !y[i] || rows[i] == 0 || cols[i] == 0) return SMOE_ERR_ARG;
+            if (cols[i] % 8 || cols[i] > smoe::GEMV_MAX_COLS || (reinterpret_cast<uintptr_t>(w[i]) & 15) ||
+                (reinterpret_cast<uintptr_t>(x[i]) & 15))
+                return SMOE_ERR_SHAPE;
+            g.w[j] = w[i];
+            g.x[j] = x[i];
+            g.y[j] = y[i];
+            g.rows[j] = rows[i];
+            g.cols[j] = cols[i];
+        }
+        if (!timed(ctx, SMOE_KERNEL_GEMV, "gemv_bf16", [&] { return smoe::launch_gemv_bf16(g, ctx->stream); }))
+            return SMOE_ERR_HIP;
+    }
+    return SMOE_OK;
+}
+
+extern "C" int smoe_hip_matvec_bf16(SmoeMetalCtx* ctx, const uint16_t* w, const float* x, float* y, uint32_t rows,
+                                    uint32_t cols)
+{
+    return smoe_hip_matvec_group_bf16(ctx, &w, &x, &y, &rows, &cols, 1);
+}
+
+extern "C" int smoe_hip_attention_layer(SmoeMetalCtx* ctx, const SmoeAttnLayerArgs* a)
+{
+    if (!ctx || !a) return SMOE_ERR_ARG;
+    if (!a->w_q || !a->w_k || !a->w_v || !a->w_o || !a->rope_cos || !a->rope_sin || !a->normed_in || !a->qbuf ||
+        !a->kbuf || !a->vbuf || !a->k_cache || !a->v_cache || !a->attn_out || !a->o_out)
+        return SMOE_ERR_ARG;
+    if (a->head_dim == 0 || a->head_dim % 64 || a->head_dim > smoe::ATTN_MAX_HEAD_DIM || a->num_heads == 0 ||
+        a->num_kv_heads == 0 || a->num_heads % a->num_kv_heads || a->q_dim != a->num_heads * a->head_dim ||
+        a->kv_dim != a->num_kv_heads * a->head_dim || a->attn_ctx == 0 || a->slot >= a->attn_ctx ||
+        a->valid == 0 || a->valid > a->attn_ctx || a->d_model == 0)
+        return SMOE_ERR_SHAPE;
+    const smoe::AttnDims dims{a->head_dim, a->num_heads, a->num_kv_heads, a->kv_dim, a->attn_ctx, a->attn_scale};
+    const size_t need = smoe::attn_part_floats(dims, a->valid);
+    if (ctx->attn_part_cap < need) {
+        if (stream_capturing(ctx->stream)) return SMOE_ERR_CAPTURE;
+        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
+        dfree(ctx->attn_part);
+        ctx->attn_part_cap = 0;
+        if (!dalloc(ctx, &ctx->attn_part, need)) return SMOE_ERR_HIP;
+        ctx->attn_part_cap = need;
+    }
+    // QKV projections in one launch (decode.cpp:151-153)
+    const uint16_t* w3[3] = {a->w_q, a->w_k, a->w_v};
+    const float* x3[3] = {a->normed_in, a->normed_in, a->normed_in};
+    float* y3[3] = {a->qbuf, a->kbuf, a->vbuf};
+    const uint32_t r3[3] = {a->q_dim, a->kv_dim, a->kv_dim};
+    const uint32_t c3[3] = {a->d_model, a->d_model, a->d_model};
+    int rc = smoe_hip_matvec_group_bf16(ctx, w3, x3, y3, r3, c3, 3);
+    if (rc != SMOE_OK) return rc;
+    if (!timed(ctx, SMOE_KERNEL_ATTENTION, "attention", [&] {
+            return smoe::launch_attention(dims, a->qbuf, a->kbuf, a->vbuf, a->q_norm_w, a->k_norm_w, a->rope_cos,
+                                          a->rope_sin, a->k_cache, a->v_cache, a->slot, a->valid, ctx->attn_part,
+                                          a->attn_out, ctx->stream);
+        }))
+        return SMOE_ERR_HIP;
+    // O projection (decode.cpp:229)
+    return smoe_hip_matvec_bf16(ctx, a->w_o, a->attn_out, a->o_out, a->d_model, a->q_dim);
+}
+
 extern "C" void smoe_metal_attention_layer(SmoeMetalCtx* ctx, const SmoeAttnLayerArgs* args)
 {
-    (void)args;
-    if (ctx) std::snprintf(ctx->last_err, sizeof(ctx->last_err), "attention_layer: not provided by this library");
-    std::fprintf(stderr, "[smoe_hip] smoe_metal_attention_layer: attention is outside this library (MoE block only)\n");
+    if (!ctx) return;
+    const int rc = smoe_hip_attention_layer(ctx, args);
+    if (rc != SMOE_OK || !hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize"))
+        std::fprintf(stderr, "[smoe_hip] attention_layer failed: %s\n", ctx->last_err);
 }
 
 extern "C" uint64_t smoe_metal_kernel_dispatches(const SmoeMetalCtx* ctx)

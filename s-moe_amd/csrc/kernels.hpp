@@ -136,6 +136,37 @@ hipError_t launch_decode_stack(const MoeDims& d, const LayerDesc* layers, uint32
 hipError_t launch_matvec_bf16(const uint16_t* W, const float* x, float* out, uint32_t rows, uint32_t cols,
                               hipStream_t s);
 
+// ---- dense trunk (trunk.hip) ---------------------------------------------
+// up to GEMV_MAX independent y = W x (bf16 W [rows x cols], fp32 x, y) in one
+// launch; cols % 8 == 0, cols <= GEMV_MAX_COLS, W and x 16-byte aligned
+constexpr uint32_t GEMV_MAX = 8;
+constexpr uint32_t GEMV_MAX_COLS = 16384;
+struct GemvGroup {
+    const uint16_t* w[GEMV_MAX];
+    const float* x[GEMV_MAX];
+    float* y[GEMV_MAX];
+    uint32_t rows[GEMV_MAX], cols[GEMV_MAX], block0[GEMV_MAX];
+    uint32_t count;
+};
+hipError_t launch_gemv_bf16(const GemvGroup& g, hipStream_t s);
+
+// single-token decode attention over a KV ring of ctx positions
+constexpr uint32_t ATTN_MAX_HEAD_DIM = 256;
+constexpr uint32_t ATTN_THREADS = 256;
+constexpr uint32_t ATTN_MAX_CHUNK = 4096;   // positions per split (scores in LDS)
+struct AttnDims {
+    uint32_t head_dim, num_heads, num_kv_heads, kv_dim, ctx;
+    float scale;
+};
+uint32_t attn_splits(const AttnDims& a, uint32_t valid);
+size_t attn_part_floats(const AttnDims& a, uint32_t valid);
+// prep (QK norm + RoPE + KV append) then attention into attn_out [q_dim];
+// part: attn_part_floats(a, valid) floats of scratch
+hipError_t launch_attention(const AttnDims& a, float* q, float* k, const float* v, const uint16_t* q_norm_w,
+                            const uint16_t* k_norm_w, const float* rope_cos, const float* rope_sin, float* k_cache,
+                            float* v_cache, uint32_t slot, uint32_t valid, float* part, float* attn_out,
+                            hipStream_t s);
+
 // ---- prefill, T token rows (moe_prefill.hip) -----------------------------
 // RMSNorm + router + top-k for T tokens: normed [T x D], ids/w [T x K].
 hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, float* normed,

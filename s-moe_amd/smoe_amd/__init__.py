@@ -67,6 +67,15 @@ class SmoeVaultInfo(C.Structure):
                 + [("rope_theta", C.c_float), ("rms_norm_eps", C.c_float), ("model_type", C.c_char * 24)])
 
 
+class SmoeAttnLayerArgs(C.Structure):
+    _fields_ = ([(n, C.c_void_p) for n in ("w_q", "w_k", "w_v", "w_o", "q_norm_w", "k_norm_w", "rope_cos",
+                                           "rope_sin", "normed_in", "qbuf", "kbuf", "vbuf", "k_cache", "v_cache",
+                                           "attn_out", "o_out")]
+                + [(n, C.c_uint32) for n in ("d_model", "q_dim", "kv_dim", "head_dim", "num_heads", "num_kv_heads",
+                                             "slot", "valid", "attn_ctx")]
+                + [("attn_scale", C.c_float)])
+
+
 class SmoeExpertBlob(C.Structure):
     _fields_ = [("packed_gate", C.c_void_p), ("scales_gate", C.c_void_p),
                 ("packed_up", C.c_void_p), ("scales_up", C.c_void_p),
@@ -90,7 +99,7 @@ SIGNATURES = [
     ("smoe_metal_scout_matvec_bf16", None, [_VP, _VP, _VP, _VP, _U32, _U32]),
     ("smoe_metal_scout_matvec_batch_bf16", None, [_VP, _VP, _VP, _VP, _VP, _VP, _U32]),
     ("smoe_metal_scout_matvec_group_bf16", None, [_VP, _VP, _VP, _VP, _VP, _VP, _U32]),
-    ("smoe_metal_attention_layer", None, [_VP, _VP]),
+    ("smoe_metal_attention_layer", None, [_VP, C.POINTER(SmoeAttnLayerArgs)]),
     ("smoe_hip_set_stream", _I, [_VP, _VP]),
     ("smoe_hip_synchronize", _I, [_VP]),
     ("smoe_hip_reserve", _I, [_VP, _SHP, _U32]),
@@ -105,6 +114,10 @@ SIGNATURES = [
     ("smoe_hip_synth_normal", _I, [_VP, _VP, _U64, _U64, _U64, _F]),
     ("smoe_hip_synth_bf16", _I, [_VP, _VP, _U64, _U64, _U64, _F]),
     ("smoe_hip_synth_expert_pool", _I, [_VP, _VP, _U32, _U32, _U32, _U64, _SHP, _U64, _F]),
+    ("smoe_hip_matvec_bf16", _I, [_VP, _VP, _VP, _VP, _U32, _U32]),
+    ("smoe_hip_matvec_group_bf16", _I, [_VP, C.POINTER(_VP), C.POINTER(_VP), C.POINTER(_VP),
+                                        C.POINTER(C.c_uint32), C.POINTER(C.c_uint32), _U32]),
+    ("smoe_hip_attention_layer", _I, [_VP, C.POINTER(SmoeAttnLayerArgs)]),
     ("smoe_hip_vault_open", _I, [C.c_char_p, C.POINTER(_VP)]),
     ("smoe_hip_vault_close", None, [_VP]),
     ("smoe_hip_vault_info", _I, [_VP, C.POINTER(SmoeVaultInfo)]),
@@ -120,10 +133,11 @@ SIGNATURES = [
 KERNEL_MOE_UP, KERNEL_GATE_UP, KERNEL_MOE_DOWN, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
 KERNEL_PERMUTE, KERNEL_GROUPED_GATE_UP, KERNEL_GROUPED_DOWN, KERNEL_SCATTER = 5, 6, 7, 8
 KERNEL_ROUTE, KERNEL_SPLIT, KERNEL_STACK, KERNEL_MOE_LAYER = 9, 10, 11, 12
+KERNEL_GEMV, KERNEL_ATTENTION = 13, 14
 DECODE_LAUNCHES, DECODE_PERSISTENT, DECODE_SPLIT = 0, 1, 2
 KERNEL_NAMES = {0: "moe_up", 1: "gate_up", 2: "moe_down", 3: "down_slots", 4: "topk",
                 5: "permute", 6: "grouped_gate_up", 7: "grouped_down", 8: "combine", 9: "route",
-                10: "split", 11: "decode_stack", 12: "moe_layer"}
+                10: "split", 11: "decode_stack", 12: "moe_layer", 13: "gemv", 14: "attention"}
 
 _lib = None
 
@@ -219,6 +233,25 @@ class Context:
         self._check(self.lib.smoe_hip_moe_prefill_stack(self.ptr, C.byref(shape), layers, len(layers), hidden,
                                                         n_tokens, ids or None, weights or None),
                     "moe_prefill_stack")
+
+    # -- dense trunk ------------------------------------------------------------
+    def matvec_bf16(self, w: int, x: int, y: int, rows: int, cols: int):
+        self._check(self.lib.smoe_hip_matvec_bf16(self.ptr, w, x, y, rows, cols), "matvec_bf16")
+
+    def matvec_group_bf16(self, ws, xs, ys, rows, cols):
+        n = len(ws)
+        arr = lambda v, t: (t * n)(*v)
+        self._check(self.lib.smoe_hip_matvec_group_bf16(self.ptr, arr(ws, C.c_void_p), arr(xs, C.c_void_p),
+                                                        arr(ys, C.c_void_p), arr(rows, C.c_uint32),
+                                                        arr(cols, C.c_uint32), n), "matvec_group_bf16")
+
+    def attention_layer(self, args: "SmoeAttnLayerArgs", sync: bool = False):
+        """smoe_hip_attention_layer (async); sync=True uses the reference-surface
+        smoe_metal_attention_layer instead (synchronous, errors to stderr)."""
+        if sync:
+            self.lib.smoe_metal_attention_layer(self.ptr, C.byref(args))
+        else:
+            self._check(self.lib.smoe_hip_attention_layer(self.ptr, C.byref(args)), "attention_layer")
 
     def set_decode_engine(self, engine: int):
         """DECODE_LAUNCHES (per-layer calls), DECODE_PERSISTENT (one launch per step) or
