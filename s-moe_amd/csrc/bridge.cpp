@@ -94,8 +94,8 @@ struct SmoeMetalCtx {
     uint32_t* d_err = nullptr;       // [1] device-side error flags (bit 0: exchange time-out, bit 1: bad expert id)
     uint32_t* perm_pairs = nullptr;  // smoe_hip_permute's sorted pair ids
     float* mv_in = nullptr;          // reference-surface GEMV staging
-    float* attn_part = nullptr;      // decode attention: per-(head, split) partials
-    size_t attn_part_cap = 0;
+    uint8_t* attn_part = nullptr;    // decode attention: per-(head, split) partials + counters
+    size_t attn_part_cap = 0;        // bytes
     float* mv_out = nullptr;
     uint32_t mv_cap = 0;
     uint64_t perm_cap = 0;
@@ -667,13 +667,14 @@ extern "C" int smoe_hip_attention_layer(SmoeMetalCtx* ctx, const SmoeAttnLayerAr
     if (!a->w_q || !a->w_k || !a->w_v || !a->w_o || !a->rope_cos || !a->rope_sin || !a->normed_in || !a->qbuf ||
         !a->kbuf || !a->vbuf || !a->k_cache || !a->v_cache || !a->attn_out || !a->o_out)
         return SMOE_ERR_ARG;
-    if (a->head_dim == 0 || a->head_dim % 64 || a->head_dim > smoe::ATTN_MAX_HEAD_DIM || a->num_heads == 0 ||
+    if ((a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) || a->num_heads == 0 ||
         a->num_kv_heads == 0 || a->num_heads % a->num_kv_heads || a->q_dim != a->num_heads * a->head_dim ||
         a->kv_dim != a->num_kv_heads * a->head_dim || a->attn_ctx == 0 || a->slot >= a->attn_ctx ||
         a->valid == 0 || a->valid > a->attn_ctx || a->d_model == 0)
         return SMOE_ERR_SHAPE;
+    if ((reinterpret_cast<uintptr_t>(a->k_cache) | reinterpret_cast<uintptr_t>(a->v_cache)) % 16) return SMOE_ERR_ARG;
     const smoe::AttnDims dims{a->head_dim, a->num_heads, a->num_kv_heads, a->kv_dim, a->attn_ctx, a->attn_scale};
-    const size_t need = smoe::attn_part_floats(dims, a->valid);
+    const size_t need = smoe::attn_scratch_bytes(dims);
     if (ctx->attn_part_cap < need) {
         if (stream_capturing(ctx->stream)) return SMOE_ERR_CAPTURE;
         if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;

@@ -240,6 +240,56 @@ __device__ __forceinline__ float seg_sum_rows(const float (&v)[N])
     return a[0];
 }
 
+// seg_sum_rows followed by the reverse butterfly: every lane returns all N
+// segment totals (out[i] = total of value i over the lane's segment).  The
+// gather runs over the split bits from the lowest up; at each bit a lane
+// doubles the values it holds with its partner's (the partner differs in that
+// bit and, for row_half_mirror, in lower bits whose values agree already).
+template <int BIT>
+__device__ __forceinline__ void gather_bit(float mine, float& lo, float& hi, int lane)
+{
+    if constexpr (BIT == 5 || BIT == 4) {
+        const auto r = BIT == 5 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(mine), __float_as_uint(mine),
+                                                                    false, false)
+                                : __builtin_amdgcn_permlane16_swap(__float_as_uint(mine), __float_as_uint(mine),
+                                                                    false, false);
+        lo = __uint_as_float(r[0]);     // the value of the half with the bit clear
+        hi = __uint_as_float(r[1]);
+    } else {
+        constexpr int CTRL = BIT == 3 ? DPP_ROW_ROR8
+                           : BIT == 2 ? DPP_ROW_HALF_MIRROR
+                           : BIT == 1 ? DPP_QUAD_XOR2
+                                      : DPP_QUAD_XOR1;
+        const float other = dpp_f32<CTRL>(0.f, mine);
+        const bool upper = lane & (1 << BIT);
+        lo = upper ? other : mine;
+        hi = upper ? mine : other;
+    }
+}
+
+template <int SEG, int N, int S = 0>
+__device__ __forceinline__ void gather_steps(float (&a)[N], int lane)
+{
+    constexpr int LOG_N = ilog2(N);
+    if constexpr (S < LOG_N) {
+        constexpr int C = 1 << S;       // values held before this step
+        float t[2 * C];
+#pragma unroll
+        for (int k = 0; k < C; ++k) gather_bit<SEG - LOG_N + S>(a[k], t[k], t[C + k], lane);
+#pragma unroll
+        for (int k = 0; k < 2 * C; ++k) a[k] = t[k];
+        gather_steps<SEG, N, S + 1>(a, lane);
+    }
+}
+
+template <int N, int SEG>
+__device__ __forceinline__ void seg_allsum(float (&v)[N])
+{
+    const int lane = threadIdx.x & 63;
+    seg_steps<SEG, N>(v, lane);
+    gather_steps<SEG, N>(v, lane);
+}
+
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 {
     v = max(v, dpp_u32<DPP_QUAD_XOR1>(0u, v));

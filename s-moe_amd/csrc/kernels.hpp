@@ -150,22 +150,28 @@ struct GemvGroup {
 };
 hipError_t launch_gemv_bf16(const GemvGroup& g, hipStream_t s);
 
-// single-token decode attention over a KV ring of ctx positions
-constexpr uint32_t ATTN_MAX_HEAD_DIM = 256;
-constexpr uint32_t ATTN_THREADS = 256;
-constexpr uint32_t ATTN_MAX_CHUNK = 4096;   // positions per split (scores in LDS)
+// single-token decode attention over a KV ring of ctx positions: one fused
+// launch (QK norm + RoPE + KV append, attention per (KV head, query-head
+// group, context split) with an online softmax), and with several splits a
+// combine launch, into attn_out [q_dim].  head_dim 64, 128 or 256.
+constexpr uint32_t ATTN_MAX_SPLITS = 64;
 struct AttnDims {
     uint32_t head_dim, num_heads, num_kv_heads, kv_dim, ctx;
     float scale;
 };
-uint32_t attn_splits(const AttnDims& a, uint32_t valid);
-size_t attn_part_floats(const AttnDims& a, uint32_t valid);
-// prep (QK norm + RoPE + KV append) then attention into attn_out [q_dim];
-// part: attn_part_floats(a, valid) floats of scratch
-hipError_t launch_attention(const AttnDims& a, float* q, float* k, const float* v, const uint16_t* q_norm_w,
-                            const uint16_t* k_norm_w, const float* rope_cos, const float* rope_sin, float* k_cache,
-                            float* v_cache, uint32_t slot, uint32_t valid, float* part, float* attn_out,
-                            hipStream_t s);
+struct AttnPlan {
+    uint32_t gb;        // query heads per block (power of two <= 8)
+    uint32_t n_sub;     // blocks per KV head along the query heads
+    uint32_t splits;    // context splits
+    uint32_t chunk;     // positions per split
+};
+AttnPlan attn_plan(const AttnDims& a, uint32_t valid);
+// scratch of the launch: per-(head, split) partials
+size_t attn_scratch_bytes(const AttnDims& a);
+hipError_t launch_attention(const AttnDims& a, const float* q, const float* k, const float* v,
+                            const uint16_t* q_norm_w, const uint16_t* k_norm_w, const float* rope_cos,
+                            const float* rope_sin, float* k_cache, float* v_cache, uint32_t slot, uint32_t valid,
+                            void* scratch, float* attn_out, hipStream_t s);
 
 // ---- prefill, T token rows (moe_prefill.hip) -----------------------------
 // RMSNorm + router + top-k for T tokens: normed [T x D], ids/w [T x K].

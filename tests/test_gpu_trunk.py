@@ -91,8 +91,24 @@ def rope(pos, head_dim, theta=1e6):
     (2048, 32, 4, 128, 1024, 700, 513, False),   # no QK norm
     (4096, 64, 4, 128, 2048, 1999, 1000, True),  # Qwen3-235B-A22B layout (16 query heads per KV head)
     (512, 8, 8, 64, 64, 5, 40, True),            # MHA, head_dim 64
+    (1024, 16, 16, 64, 2048, 100, 1500, True),   # MHA, several context splits
+    (2048, 8, 2, 256, 512, 300, 400, True),      # head_dim 256
+    (1280, 10, 2, 128, 1024, 50, 800, False),    # 5 query heads per KV head (padded group)
 ])
 def test_attention_layer_vs_oracle(ctx, oracle, d_model, nh, nkv, hd, ctx_len, slot, valid, qk):
+    run_attention_case(ctx, oracle, d_model, nh, nkv, hd, ctx_len, slot, valid, qk)
+
+
+def test_attention_scratch_reuse(ctx, oracle):
+    """Shapes that grow, shrink and grow the context's split scratch in turn:
+    the split counters must survive every reuse."""
+    for case in ((4096, 64, 4, 128, 2048, 1999, 1000, True), (2048, 8, 2, 256, 512, 300, 400, True),
+                 (512, 8, 8, 64, 1024, 5, 900, False), (4096, 64, 4, 128, 2048, 7, 2048, True)):
+        run_attention_case(ctx, oracle, *case)
+
+
+def run_attention_case(ctx, oracle, d_model, nh, nkv, hd, ctx_len, slot, valid, qk):
+    print(f"case attention d={d_model} heads={nh}/{nkv}x{hd} ctx={ctx_len} slot={slot} valid={valid}", flush=True)
     q_dim, kv_dim = nh * hd, nkv * hd
     W = {n: bf16_weights(ctx, r, c, 7300 + i) for i, (n, (r, c)) in enumerate(
         dict(q=(q_dim, d_model), k=(kv_dim, d_model), v=(kv_dim, d_model), o=(d_model, q_dim)).items())}
@@ -141,3 +157,45 @@ def test_attention_layer_vs_oracle(ctx, oracle, d_model, nh, nkv, hd, ctx_len, s
     dev["o"].zero_()
     ctx.attention_layer(a, sync=True)
     assert torch.equal(dev["o"], o_async)
+
+
+def test_attention_decode_steps(ctx, oracle):
+    """Five consecutive tokens through one ring (the split counters and the KV
+    append carry from call to call), each output against the oracle run on
+    the oracle's own ring."""
+    d_model, nh, nkv, hd, ctx_len = 2048, 32, 4, 128, 1024
+    q_dim, kv_dim = nh * hd, nkv * hd
+    W = {n: bf16_weights(ctx, r, c, 7400 + i) for i, (n, (r, c)) in enumerate(
+        dict(q=(q_dim, d_model), k=(kv_dim, d_model), v=(kv_dim, d_model), o=(d_model, q_dim)).items())}
+    kc = randn(ctx_len * kv_dim, 12).reshape(ctx_len, kv_dim).cuda()
+    vc = randn(ctx_len * kv_dim, 13).reshape(ctx_len, kv_dim).cuda()
+    kc_ref, vc_ref = kc.cpu().numpy(), vc.cpu().numpy()
+    h16 = lambda t: t.cpu().numpy().view(np.uint16)
+    dev = dict(q=torch.zeros(q_dim, device="cuda"), k=torch.zeros(kv_dim, device="cuda"),
+               v=torch.zeros(kv_dim, device="cuda"), att=torch.zeros(q_dim, device="cuda"),
+               o=torch.zeros(d_model, device="cuda"))
+    for step, (slot, valid) in enumerate(((1020, 700), (1021, 701), (1022, 702), (1023, 703), (0, 704))):
+        print(f"case decode step {step} slot={slot} valid={valid}", flush=True)
+        cos, sin = rope(5000 + step, hd)
+        x = randn(d_model, 40 + step).cuda()
+        cos_d, sin_d = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+        a = smoe_amd.SmoeAttnLayerArgs()
+        a.w_q, a.w_k, a.w_v, a.w_o = (W[n].data_ptr() for n in "qkvo")
+        a.q_norm_w = a.k_norm_w = None
+        a.rope_cos, a.rope_sin, a.normed_in = cos_d.data_ptr(), sin_d.data_ptr(), x.data_ptr()
+        a.qbuf, a.kbuf, a.vbuf = dev["q"].data_ptr(), dev["k"].data_ptr(), dev["v"].data_ptr()
+        a.k_cache, a.v_cache, a.attn_out, a.o_out = kc.data_ptr(), vc.data_ptr(), dev["att"].data_ptr(), dev["o"].data_ptr()
+        a.d_model, a.q_dim, a.kv_dim, a.head_dim, a.num_heads, a.num_kv_heads = d_model, q_dim, kv_dim, hd, nh, nkv
+        a.slot, a.valid, a.attn_ctx, a.attn_scale = slot, valid, ctx_len, 1.0 / np.sqrt(hd)
+        ctx.attention_layer(a)
+        ctx.synchronize()
+        o_ref, kc_ref, vc_ref = oracle.attention_layer(h16(W["q"]), h16(W["k"]), h16(W["v"]), h16(W["o"]), None, None,
+                                                       cos, sin, x.cpu().numpy(), kc_ref, vc_ref, hd, nh, nkv, slot,
+                                                       valid, 1.0 / np.sqrt(hd))
+        e_o, _ = rel_err(dev["o"].cpu().numpy(), o_ref)
+        e_k, _ = rel_err(kc.cpu().numpy()[slot], kc_ref[slot])
+        print(f"  rel_err o={e_o:.2e} k={e_k:.2e}")
+        assert e_o <= TOL_ATTN and e_k <= TOL_ATTN
+        # keep the two rings identical so the next step compares like with like
+        kc.copy_(torch.from_numpy(kc_ref))
+        vc.copy_(torch.from_numpy(vc_ref))
