@@ -311,40 +311,59 @@ void k_permute(const uint32_t* __restrict__ ids, const float* __restrict__ w, ui
 
 // ---------------------------------------------------------------------------
 // k_grouped_mm: for each expert e with M = offsets[e+1] - offsets[e] pairs,
-// out[pair][n] for a 64-row tile of its weight matrix (gate+up or down).
-// Block = 4 waves; wave w owns rows n0 + 16 w .. + 16 (one MFMA tile); a pass
-// covers 64 pairs as four 16-row tiles (one pass for up to 64 pairs, so each
-// weight is read and converted once per expert).  The k dimension runs in
-// chunks of 128 columns: the block stages the chunk's activation rows (f16 hi
-// and lo planes) in LDS once for its 4 waves, and the next chunk's weights and
-// activation rows are loaded into registers while the current chunk computes.
+// out[pair][n] for one tile of its weight matrix: 128 rows of gate and of up
+// (gate+up, SiLU fused) or 256 rows of down.  Block = 8 waves; wave w owns two
+// 16-row MFMA subtiles (gate and up rows 16w.., or down rows 32w.. and
+// 32w + 16..) and all m-tiles of the pass (up to 64 pairs, so each weight is
+// read once per expert for M <= 64).
+//
+// The k dimension streams through two rings in LDS, filled by direct
+// global->LDS loads (global_load_lds_dwordx4) so that nothing in flight holds
+// registers:
+//   weights      GM_SW stages of two 64-column groups: every wave brings its
+//                32 rows x 64 bytes of codes (each row's 64 bytes in one
+//                instruction: 32-byte pieces per row halve the stream rate)
+//                and the rows' two fp16 scales;
+//   activations  GM_SA stages of one group: the pass's rows (f16 hi and lo
+//                planes), a share per wave.
+// Body c (one group) waits for its stages, passes one barrier, requests weight
+// stage c/2 + 3 (even c) and activation stage c + 3, and computes.  Each stage
+// lives in its own __shared__ object, so the compiler can tell the in-flight
+// fills from the stage being read; completion is awaited with an explicit
+// vmcnt: every wave issues the same loads in the same order.
 //
 // v_mfma_f32_16x16x32_f16 operand layout: lane l holds A[l % 16][8 (l/16) + j]
 // and B[8 (l/16) + j][l % 16] (j < 8) and receives D[4 (l/16) + i][l % 16].
 // Inside a 64-column group, lane quarter q = l/16 of MFMA step s uses the
-// physical columns 16 q + 8 s + j, so each lane reads 8 contiguous bytes of
-// packed weights per group.  Weights enter as f16 (2c - 15) (exact), so a
-// group's MFMA sum times s_g is 15/7.5 of its dequantised dot product
+// physical columns 16 q + 8 s + j.  Weights enter as f16 (2c - 15) (exact), so
+// a group's MFMA sum times s_g is 15/7.5 of its dequantised dot product
 // (kernels.metal:90-105, 140-145) and the epilogue is one FMA per output.
+// LDS layouts (16-byte slots; XOR swizzles keep the fragment reads free of
+// bank conflicts):
+//   weights  subtile j of wave w: row n, slot (2 g + h) ^ (n >> 2 & 3) holds
+//            bytes 16 h .. 16 h + 15 of group g of the stage;
+//   acts     row r, slot x ^ (r & 15) = logical slot x = 8 plane + c8, i.e.
+//            columns 8 c8 .. 8 c8 + 7 of the group in plane hi (0) or lo (1).
 // ---------------------------------------------------------------------------
-constexpr int MM_WAVES = 4;
-constexpr int MM_NS = 1;                          // 16-row weight tiles per wave
-constexpr int MM_ROWS = 16 * MM_NS * MM_WAVES;    // weight rows per block
-constexpr int MM_MS = 4;                          // 16-pair tiles per pass
-constexpr int MM_PASS = 16 * MM_MS;               // pairs per pass
-constexpr int MM_KC = 128;                        // columns per chunk (2 groups)
-constexpr int MM_GC = MM_KC / 64;
-constexpr int MM_LDS_ROW = MM_KC + 8;             // f16 per staged row (+16 B: spreads LDS banks)
+constexpr int GM_WAVES = 8;
+constexpr int GM_SW = 4;                     // weight ring stages (two 64-column groups each)
+constexpr int GM_SA = 4;                     // activation ring stages (one group each)
+constexpr int GM_PASS = 64;                  // pair rows per pass (4 m-tiles)
+constexpr uint32_t GM_ROWS_GU = 16 * GM_WAVES;   // gate (and up) rows per block
+constexpr uint32_t GM_ROWS_DN = 32 * GM_WAVES;   // down rows per block
 
-// eight codes (one dword, low nibble first) -> f16 (2c - 15), exact.
-// The bias is added to the whole half8 at once: assembling the half8 element
-// by element from four half2 sums was miscompiled by this toolchain (hipcc
-// 7.2, gfx950: the four pairs collapsed into copies of the first).
+struct GmW {                                 // one weight stage: 2 groups of the block's rows
+    uint8_t w[GM_WAVES * 2048];              // per wave: subtile j (1 KB) = 16 rows x 4 slots of 16 B
+    uint32_t sc[GM_WAVES * 64];              // per wave: slot 32 g + 16 j + n holds the fp16 scale
+};
+struct GmA { uint8_t a[GM_PASS * 256]; };    // one activation stage: row = 16 slots (hi, lo) x 64 columns
+
+#define SMOE_LDS_AS(p) ((__attribute__((address_space(3))) void*)(p))
+
 __device__ __forceinline__ half8_t q4_codes_to_f16(uint32_t v)
 {
-    const uint32_t E = v & 0x0F0F0F0Fu;          // codes 0, 2, 4, 6
-    const uint32_t O = (v >> 4) & 0x0F0F0F0Fu;   // codes 1, 3, 5, 7
-    // f16 bits 0x6400 | 2c = 1024 + 2c exactly; minus 1039 -> 2c - 15 exactly
+    const uint32_t E = v & 0x0F0F0F0Fu;
+    const uint32_t O = (v >> 4) & 0x0F0F0F0Fu;
     u32x4_t r;
     r.x = (__builtin_amdgcn_perm(O, E, 0x0C040C00u) << 1) | 0x64006400u;
     r.y = (__builtin_amdgcn_perm(O, E, 0x0C050C01u) << 1) | 0x64006400u;
@@ -355,7 +374,7 @@ __device__ __forceinline__ half8_t q4_codes_to_f16(uint32_t v)
     return __builtin_bit_cast(half8_t, r) + bias;
 }
 
-__device__ __forceinline__ half8_t lds_half8(const uint16_t* p)
+__device__ __forceinline__ half8_t lds_half8(const uint8_t* p)
 {
     const uint4 v = *reinterpret_cast<const uint4*>(__builtin_assume_aligned(p, 16));
     u32x4_t u;
@@ -363,44 +382,74 @@ __device__ __forceinline__ half8_t lds_half8(const uint16_t* p)
     return __builtin_bit_cast(half8_t, u);
 }
 
+template <int N>
+__device__ __forceinline__ void vm_wait()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ void mem_fence_compiler() { asm volatile("" ::: "memory"); }
+__device__ __forceinline__ void gm_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 template <bool GATE_UP, int MS>
 __device__ __forceinline__ void grouped_mm_expert(
     const MoeDims& d, const LayerDesc& L, uint32_t e, uint32_t tile, uint32_t base, uint32_t M,
     const uint32_t* __restrict__ sorted_pairs, const uint16_t* __restrict__ a_hi, const uint16_t* __restrict__ a_lo,
     const float* __restrict__ a_scale, uint32_t a_row_div, float* __restrict__ out, uint32_t n_dim, uint32_t k_dim,
-    uint16_t (&s_a)[2][MM_PASS][MM_LDS_ROW], uint32_t (&s_row)[MM_PASS], uint32_t (&s_pair)[MM_PASS])
+    GmW& w0, GmW& w1, GmW& w2, GmW& w3, GmA& a0, GmA& a1, GmA& a2, GmA& a3, uint32_t (&s_row)[GM_PASS],
+    uint32_t (&s_pair)[GM_PASS])
 {
-    constexpr int NM = GATE_UP ? 2 : 1;
+    constexpr int AN = MS == 4 ? 2 : 1;          // activation loads per wave and stage (4 rows each)
     constexpr int PASS = 16 * MS;
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-
+    const int lane = threadIdx.x & 63;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t G = k_dim >> 6;
-    const uint32_t q = lane >> 4;
-    uint32_t n[MM_NS];
-    bool n_ok[MM_NS];
-#pragma unroll
-    for (int ns = 0; ns < MM_NS; ++ns) {
-        const uint32_t r = tile * MM_ROWS + wv * (16 * MM_NS) + ns * 16 + (lane & 15);
-        n_ok[ns] = r < n_dim;
-        n[ns] = min(r, n_dim - 1);
-    }
+    const uint32_t m16 = lane & 15, q = lane >> 4;
+
     const uint8_t* blob = L.experts + static_cast<size_t>(e) * L.stride;
-    const uint8_t* wp[NM];
-    const uint16_t* sp[NM];
-    if (GATE_UP) {
-        wp[0] = blob + L.off[0];
-        sp[0] = reinterpret_cast<const uint16_t*>(blob + L.off[1]);
-        wp[NM - 1] = blob + L.off[2];
-        sp[NM - 1] = reinterpret_cast<const uint16_t*>(blob + L.off[3]);
-    } else {
-        wp[0] = blob + L.off[4];
-        sp[0] = reinterpret_cast<const uint16_t*>(blob + L.off[5]);
-    }
     const size_t row_bytes = k_dim >> 1;
-    // staging role of this thread: rows tm and tm + 32, 32 columns at ts * 32
-    // of each chunk (4 threads per row and chunk)
-    const uint32_t tm = threadIdx.x >> 2, ts = threadIdx.x & 3;
-    const uint32_t nck = (k_dim + MM_KC - 1) / MM_KC;
+    auto w_row = [&](uint32_t j, uint32_t n) -> uint32_t {
+        const uint32_t r = GATE_UP ? tile * GM_ROWS_GU + 16 * wv + n : tile * GM_ROWS_DN + 32 * wv + 16 * j + n;
+        return min(r, n_dim - 1);
+    };
+    auto w_mat = [&](uint32_t j) -> const uint8_t* { return blob + (GATE_UP ? (j ? L.off[2] : L.off[0]) : L.off[4]); };
+    auto s_mat = [&](uint32_t j) -> const uint16_t* {
+        return reinterpret_cast<const uint16_t*>(blob + (GATE_UP ? (j ? L.off[3] : L.off[1]) : L.off[5]));
+    };
+    // weight fill, instruction j: lane -> row n = lane / 4, physical slot p = lane & 3,
+    // logical slot s = p ^ (n / 4 & 3) = 2 g + h: bytes 32 g + 16 h of the stage's 64
+    const uint32_t fn = lane >> 2, fs = (lane & 3) ^ ((fn >> 2) & 3);
+    const uint32_t fg = fs >> 1, fh = fs & 1;
+    const uint8_t* w_src[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) w_src[j] = w_mat(j) + static_cast<size_t>(w_row(j, fn)) * row_bytes + 16 * fh;
+    // scale fill: lane -> group g = lane / 32 of the stage, subtile (lane / 16) & 1, row lane & 15
+    const uint32_t sg = lane >> 5, sj = (lane >> 4) & 1, sn = lane & 15;
+    const uint16_t* s_src = s_mat(sj) + static_cast<size_t>(w_row(sj, sn)) * G;
+    // (an odd G's last stage has one group: its second group re-reads group G - 1)
+    auto issue_w = [&](GmW& S, uint32_t st) {
+        const uint32_t g0 = 2 * st + fg, gs = 2 * st + sg;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            __builtin_amdgcn_global_load_lds(w_src[j] + min(g0, G - 1) * 32, SMOE_LDS_AS(&S.w[wv * 2048 + j * 1024]),
+                                             16, 0, 0);
+        __builtin_amdgcn_global_load_lds(s_src + min(gs, G - 1), SMOE_LDS_AS(&S.sc[wv * 64]), 2, 0, 0);
+    };
+    // B fragment of this lane for group g of a stage: row m16, bytes 8 q .. 8 q + 7 of the group
+    uint32_t boff[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) boff[g] = wv * 2048 + m16 * 64 + 16 * ((2 * g + (q >> 1)) ^ ((m16 >> 2) & 3)) + 8 * (q & 1);
+    // A fragment offsets of this lane inside an activation stage (m-tile ms adds 4096 bytes)
+    uint32_t aoff[2][2];
+#pragma unroll
+    for (int stp = 0; stp < 2; ++stp)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) aoff[stp][pl] = m16 * 256 + 16 * ((8 * pl + 2 * q + stp) ^ m16);
 
     for (uint32_t m0 = 0; m0 < M; m0 += PASS) {
         __syncthreads();
@@ -410,106 +459,88 @@ __device__ __forceinline__ void grouped_mm_expert(
             s_row[threadIdx.x] = p / a_row_div;
         }
         __syncthreads();
-        const size_t arow = static_cast<size_t>(s_row[min(tm, static_cast<uint32_t>(PASS - 1))]) * k_dim;
-
-        // chunk loaders: weights (per wave) and this thread's activation share
-        uint2 wq[2][MM_NS][NM][MM_GC];
-        uint16_t sq[2][MM_NS][NM][MM_GC];
-        uint4 ah[4], al[4];
-        auto load_chunk = [&](uint32_t c, int buf_rt) {
-            const int buf = buf_rt;
-            const uint32_t kc = c * MM_KC;
-            const uint32_t gc = min(static_cast<uint32_t>(MM_KC), k_dim - kc) >> 6;
+        const uint16_t* a_src[AN];
 #pragma unroll
-            for (int ns = 0; ns < MM_NS; ++ns)
+        for (int u = 0; u < AN; ++u) {
+            const uint32_t r = wv * 4 * AN + 4 * u + (lane >> 4);
+            const uint32_t x = (lane & 15) ^ (r & 15);
+            const uint32_t srow = s_row[min(r, static_cast<uint32_t>(PASS - 1))];
+            a_src[u] = ((x >> 3) ? a_lo : a_hi) + static_cast<size_t>(srow) * k_dim + 8 * (x & 7);
+        }
+        auto issue_a = [&](GmA& S, uint32_t c) {
 #pragma unroll
-                for (int mt = 0; mt < NM; ++mt)
-#pragma unroll
-                    for (int g = 0; g < MM_GC; ++g) {
-                        const uint32_t gg = min(static_cast<uint32_t>(g), gc - 1);
-                        const u32x2_t* wr = reinterpret_cast<const u32x2_t*>(
-                            wp[mt] + n[ns] * row_bytes + (kc >> 1) + gg * 32 + 8 * q);
-                        const u32x2_t w2 = __builtin_nontemporal_load(gptr(wr));
-                        wq[buf][ns][mt][g] = make_uint2(w2.x, w2.y);
-                        sq[buf][ns][mt][g] =
-                            load_stream_u16(sp[mt] + static_cast<size_t>(n[ns]) * G + (kc >> 6) + gg);
-                    }
-            const uint32_t col = kc + min(ts * 32, gc * 64 - 32);
-            if (tm >= static_cast<uint32_t>(PASS)) return;   // rows past this pass width stay unused
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                ah[2 * i] = load_u4(a_hi + arow + col + 16 * i);
-                ah[2 * i + 1] = load_u4(a_hi + arow + col + 16 * i + 8);
-                al[2 * i] = load_u4(a_lo + arow + col + 16 * i);
-                al[2 * i + 1] = load_u4(a_lo + arow + col + 16 * i + 8);
-            }
+            for (int u = 0; u < AN; ++u)
+                __builtin_amdgcn_global_load_lds(a_src[u] + c * 64, SMOE_LDS_AS(&S.a[(wv * 4 * AN + 4 * u) * 256]), 16,
+                                                 0, 0);
         };
 
-        f32x4_t acc[MS][MM_NS][NM];
+        f32x4_t acc[MS][2];
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-            for (int ns = 0; ns < MM_NS; ++ns)
-#pragma unroll
-                for (int mt = 0; mt < NM; ++mt) acc[ms][ns][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < 2; ++j) acc[ms][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-        // one chunk: stage its activations, start the next chunk's loads, compute
-        auto step = [&](uint32_t c, auto cur_tag) {
-            constexpr int CUR = decltype(cur_tag)::value;
-            const uint32_t gc = min(static_cast<uint32_t>(MM_KC), k_dim - c * MM_KC) >> 6;
-            __syncthreads();                     // the previous chunk's readers are done
-            if (ts * 32 < gc * 64 && tm < static_cast<uint32_t>(PASS)) {
+        // Issue order of the loop: body c issues the weight stage c / 2 + 3 (if c is even)
+        // and then the activation stage c + 3.  The prologue replays bodies -6 .. -1.
+        const uint32_t NWS = (G + 1) / 2;        // weight stages
+        if (0 < NWS) issue_w(w0, 0);
+        if (1 < NWS) issue_w(w1, 1);
+        if (0 < G) issue_a(a0, 0);
+        if (2 < NWS) issue_w(w2, 2);
+        if (1 < G) issue_a(a1, 1);
+        if (2 < G) issue_a(a2, 2);
+        mem_fence_compiler();
+
+        auto body = [&](uint32_t c, GmW& W, uint32_t g, GmW& WN, GmA& A, GmA& AN_) {
+            // A(c) was the last load of body c - 3; bodies c - 2 and c - 1 issued A(c + 1),
+            // A(c + 2) and, in the even one of them, the weight stage (c + 4 + (c & 1)) / 2.
+            // When all of those were issued, 2 AN + 3 loads may still be pending; near the
+            // end fewer were, and the wait covers everything.
+            if (c + 2 < G && (c + 4 + (c & 1)) / 2 < NWS) vm_wait<2 * AN + 3>();
+            else vm_wait<0>();
+            gm_barrier();
+            if (g == 0 && c / 2 + 3 < NWS) issue_w(WN, c / 2 + 3);
+            if (c + 3 < G) issue_a(AN_, c + 3);
+            mem_fence_compiler();
+            half8_t b[2][2];
+            float sc[2];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    *reinterpret_cast<uint4*>(&s_a[0][tm][ts * 32 + 8 * i]) = ah[i];
-                    *reinterpret_cast<uint4*>(&s_a[1][tm][ts * 32 + 8 * i]) = al[i];
+            for (int j = 0; j < 2; ++j) {
+                const uint2 v = *reinterpret_cast<const uint2*>(&W.w[boff[g] + 1024 * j]);
+                b[j][0] = q4_codes_to_f16(v.x);
+                b[j][1] = q4_codes_to_f16(v.y);
+                sc[j] = f16_bits_to_f32(static_cast<uint16_t>(W.sc[wv * 64 + 32 * g + 16 * j + m16]));
+            }
+#pragma unroll
+            for (int ms = 0; ms < MS; ++ms) {
+                half8_t xa[2][2];
+#pragma unroll
+                for (int stp = 0; stp < 2; ++stp)
+#pragma unroll
+                    for (int pl = 0; pl < 2; ++pl) xa[stp][pl] = lds_half8(A.a + ms * 4096 + aoff[stp][pl]);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[0][0], b[j][0], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[0][1], b[j][0], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1][0], b[j][1], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1][1], b[j][1], t, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[ms][j][i] = fmaf(sc[j], t[i], acc[ms][j][i]);
                 }
             }
-            __syncthreads();
-            if (c + 1 < nck) load_chunk(c + 1, CUR ^ 1);   // in flight while this chunk computes
-#pragma unroll
-            for (int g = 0; g < MM_GC; ++g) {
-                if (static_cast<uint32_t>(g) >= gc) break;
-                half8_t b[MM_NS][NM][2];
-                float sc[MM_NS][NM];
-#pragma unroll
-                for (int ns = 0; ns < MM_NS; ++ns)
-#pragma unroll
-                    for (int mt = 0; mt < NM; ++mt) {
-                        b[ns][mt][0] = q4_codes_to_f16(wq[CUR][ns][mt][g].x);
-                        b[ns][mt][1] = q4_codes_to_f16(wq[CUR][ns][mt][g].y);
-                        sc[ns][mt] = f16_bits_to_f32(sq[CUR][ns][mt][g]);
-                    }
-#pragma unroll
-                for (int ms = 0; ms < MS; ++ms) {
-                    half8_t xa[2][2];   // [step][hi/lo]
-#pragma unroll
-                    for (int st = 0; st < 2; ++st)
-#pragma unroll
-                        for (int pl = 0; pl < 2; ++pl)
-                            xa[st][pl] = lds_half8(&s_a[pl][16 * ms + (lane & 15)][g * 64 + 16 * q + 8 * st]);
-#pragma unroll
-                    for (int ns = 0; ns < MM_NS; ++ns)
-#pragma unroll
-                        for (int mt = 0; mt < NM; ++mt) {
-                            f32x4_t t = {0.f, 0.f, 0.f, 0.f};
-                            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[0][0], b[ns][mt][0], t, 0, 0, 0);
-                            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[0][1], b[ns][mt][0], t, 0, 0, 0);
-                            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1][0], b[ns][mt][1], t, 0, 0, 0);
-                            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1][1], b[ns][mt][1], t, 0, 0, 0);
-#pragma unroll
-                            for (int i = 0; i < 4; ++i)
-                                acc[ms][ns][mt][i] = fmaf(sc[ns][mt], t[i], acc[ms][ns][mt][i]);
-                        }
-                }
-            }
+            mem_fence_compiler();
         };
-        load_chunk(0, 0);
-        for (uint32_t c = 0; c < nck; c += 2) {
-            step(c, std::integral_constant<int, 0>{});
-            if (c + 1 < nck) step(c + 1, std::integral_constant<int, 1>{});
+        for (uint32_t c = 0; c < G; c += 8) {
+            body(c, w0, 0, w3, a0, a3);
+            if (c + 1 < G) body(c + 1, w0, 1, w3, a1, a0);
+            if (c + 2 < G) body(c + 2, w1, 0, w0, a2, a1);
+            if (c + 3 < G) body(c + 3, w1, 1, w0, a3, a2);
+            if (c + 4 < G) body(c + 4, w2, 0, w1, a0, a3);
+            if (c + 5 < G) body(c + 5, w2, 1, w1, a1, a0);
+            if (c + 6 < G) body(c + 6, w3, 0, w2, a2, a1);
+            if (c + 7 < G) body(c + 7, w3, 1, w2, a3, a2);
         }
-        // outputs: pair rows 4 q + i of each tile, columns n; value = acc * 2^e_row / 15
 #pragma unroll
         for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
@@ -518,16 +549,17 @@ __device__ __forceinline__ void grouped_mm_expert(
                 if (m0 + m >= M) continue;
                 const float rs = a_scale[s_row[m]] * (1.0f / 15.0f);
                 float* o = out + static_cast<size_t>(s_pair[m]) * n_dim;
+                if (GATE_UP) {
+                    const uint32_t n = tile * GM_ROWS_GU + 16 * wv + m16;
+                    if (n < n_dim) {
+                        const float v0 = acc[ms][0][i] * rs, v1 = acc[ms][1][i] * rs;
+                        o[n] = (v0 * (1.0f / (1.0f + expf(-v0)))) * v1;
+                    }
+                } else {
 #pragma unroll
-                for (int ns = 0; ns < MM_NS; ++ns) {
-                    if (!n_ok[ns]) continue;
-                    const float v0 = acc[ms][ns][0][i] * rs;
-                    if (GATE_UP) {
-                        const float v1 = acc[ms][ns][NM - 1][i] * rs;
-                        // h = silu(g) * u, silu(z) = z * (1 / (1 + exp(-z)))  (kernels.metal:61-63)
-                        o[n[ns]] = (v0 * (1.0f / (1.0f + expf(-v0)))) * v1;
-                    } else {
-                        o[n[ns]] = v0;
+                    for (int j = 0; j < 2; ++j) {
+                        const uint32_t n = tile * GM_ROWS_DN + 32 * wv + 16 * j + m16;
+                        if (n < n_dim) o[n] = acc[ms][j][i] * rs;
                     }
                 }
             }
@@ -536,30 +568,30 @@ __device__ __forceinline__ void grouped_mm_expert(
 }
 
 template <bool GATE_UP>
-__global__ __launch_bounds__(MM_WAVES * WAVE, 2)
+__global__ __launch_bounds__(GM_WAVES * WAVE, 1)
 void k_grouped_mm(MoeDims d, LayerDesc L, const uint32_t* __restrict__ offsets,
                   const uint32_t* __restrict__ sorted_pairs, const uint16_t* __restrict__ a_hi,
                   const uint16_t* __restrict__ a_lo, const float* __restrict__ a_scale, uint32_t a_row_div,
                   float* __restrict__ out, uint32_t n_dim, uint32_t k_dim, uint32_t n_tiles)
 {
-    __shared__ __align__(16) uint16_t s_a[2][MM_PASS][MM_LDS_ROW];
-    __shared__ uint32_t s_row[MM_PASS];
-    __shared__ uint32_t s_pair[MM_PASS];
+    __shared__ __align__(16) GmW w0, w1, w2, w3;
+    __shared__ __align__(16) GmA a0, a1, a2, a3;
+    __shared__ uint32_t s_row[GM_PASS];
+    __shared__ uint32_t s_pair[GM_PASS];
     const uint32_t b = blockIdx.x, xcd = b & 7u, jb = b >> 3;
     const uint32_t e = xcd + 8u * (jb / n_tiles), tile = jb % n_tiles;
     if (e >= d.E) return;
     const uint32_t base = offsets[e], M = offsets[e + 1] - base;
     if (M == 0) return;
-    // pass width by the expert's pair count: MFMA rows past M are wasted work
     if (M <= 16)
         grouped_mm_expert<GATE_UP, 1>(d, L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, a_row_div, out,
-                                      n_dim, k_dim, s_a, s_row, s_pair);
+                                      n_dim, k_dim, w0, w1, w2, w3, a0, a1, a2, a3, s_row, s_pair);
     else if (M <= 32)
         grouped_mm_expert<GATE_UP, 2>(d, L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, a_row_div, out,
-                                      n_dim, k_dim, s_a, s_row, s_pair);
+                                      n_dim, k_dim, w0, w1, w2, w3, a0, a1, a2, a3, s_row, s_pair);
     else
-        grouped_mm_expert<GATE_UP, MM_MS>(d, L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, a_row_div, out,
-                                          n_dim, k_dim, s_a, s_row, s_pair);
+        grouped_mm_expert<GATE_UP, 4>(d, L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, a_row_div, out,
+                                      n_dim, k_dim, w0, w1, w2, w3, a0, a1, a2, a3, s_row, s_pair);
 }
 
 // ---------------------------------------------------------------------------
@@ -638,8 +670,8 @@ hipError_t launch_grouped_gate_up(const MoeDims& d, const LayerDesc& L, const ui
                                   const float* x_scale, float* h, hipStream_t s)
 {
     if (d.group != 64 || d.I % 64 || d.D % 64) return hipErrorInvalidValue;
-    const uint32_t n_tiles = (d.I + MM_ROWS - 1) / MM_ROWS, eg = (d.E + 7) / 8;
-    launch_kernel(k_grouped_mm<true>, dim3(8 * eg * n_tiles), dim3(MM_WAVES * WAVE), s, d, L, offsets, sorted_pairs,
+    const uint32_t n_tiles = (d.I + GM_ROWS_GU - 1) / GM_ROWS_GU, eg = (d.E + 7) / 8;
+    launch_kernel(k_grouped_mm<true>, dim3(8 * eg * n_tiles), dim3(GM_WAVES * WAVE), s, d, L, offsets, sorted_pairs,
                   x_hi, x_lo, x_scale, d.K, h, d.I, d.D, n_tiles);
     return hipGetLastError();
 }
@@ -649,8 +681,8 @@ hipError_t launch_grouped_down(const MoeDims& d, const LayerDesc& L, const uint3
                                const float* h_scale, float* y, hipStream_t s)
 {
     if (d.group != 64 || d.D % 64 || d.I % 64) return hipErrorInvalidValue;
-    const uint32_t n_tiles = (d.D + MM_ROWS - 1) / MM_ROWS, eg = (d.E + 7) / 8;
-    launch_kernel(k_grouped_mm<false>, dim3(8 * eg * n_tiles), dim3(MM_WAVES * WAVE), s, d, L, offsets,
+    const uint32_t n_tiles = (d.D + GM_ROWS_DN - 1) / GM_ROWS_DN, eg = (d.E + 7) / 8;
+    launch_kernel(k_grouped_mm<false>, dim3(8 * eg * n_tiles), dim3(GM_WAVES * WAVE), s, d, L, offsets,
                   sorted_pairs, h_hi, h_lo, h_scale, 1u, y, d.D, d.I, n_tiles);
     return hipGetLastError();
 }
