@@ -239,59 +239,118 @@ void k_permute(const uint32_t* __restrict__ ids, const float* __restrict__ w, ui
 
     for (uint32_t i = threadIdx.x; i < C * E; i += PERM_THREADS) s_cnt[i] = 0;
     for (uint32_t i = threadIdx.x; i < E; i += PERM_THREADS) s_first[i] = 0xFFFFFFFFu;
+    // each wave takes chunks wv, wv + NW, ...; the ids of up to PERM_BATCH of
+    // them are loaded together (one memory round trip), and kept for the
+    // scatter when one batch covers all of the wave's chunks
+    constexpr int PERM_BATCH = 8;
+    const bool one_batch = C <= NW * PERM_BATCH;
+    uint32_t eid[PERM_BATCH];
+    auto load_ids = [&](uint32_t c_first) {
+#pragma unroll
+        for (int k = 0; k < PERM_BATCH; ++k) {
+            const uint32_t p = (c_first + k * NW) * 64 + lane;
+            eid[k] = p < P ? ids[p] : 0xFFFFFFFFu;
+        }
+    };
     __syncthreads();
-    for (uint32_t c = wv; c < C; c += NW) {
-        const uint32_t p = c * 64 + lane;
-        if (p < P) {
-            const uint32_t e = ids[p];
+    for (uint32_t cb = wv; cb < C; cb += NW * PERM_BATCH) {
+        load_ids(cb);
+#pragma unroll
+        for (int k = 0; k < PERM_BATCH; ++k) {
+            const uint32_t c = cb + k * NW, p = c * 64 + lane;
+            if (c >= C || p >= P) continue;
+            const uint32_t e = eid[k];
             if (e < E) {
                 atomicAdd(&s_cnt[c * E + e], 1u);
-                atomicMin(&s_first[e], p);
+                if (union_ids) atomicMin(&s_first[e], p);
             } else {
                 atomicOr(err, 2u);
             }
         }
     }
     __syncthreads();
-    // per expert: counts -> exclusive prefix over chunks
-    for (uint32_t e = threadIdx.x; e < E; e += PERM_THREADS) {
-        uint32_t run = 0;
-        for (uint32_t c = 0; c < C; ++c) {
-            const uint32_t t = s_cnt[c * E + e];
-            s_cnt[c * E + e] = run;
-            run += t;
+    // per expert: counts -> exclusive prefix over chunks.  S threads (a power
+    // of two, in one wave) share an expert's C chunks in segments: segment sums,
+    // an exclusive scan over the segments, then each chunk's prefix.
+    {
+        uint32_t S = 64;
+        while (S > 1 && E * S > PERM_THREADS) S >>= 1;
+        const uint32_t e = threadIdx.x / S, sg = threadIdx.x % S;
+        const uint32_t Lc = (C + S - 1) / S;
+        const uint32_t c0 = min(sg * Lc, C), c1 = min(c0 + Lc, C);
+        uint32_t seg = 0;
+        if (e < E)
+            for (uint32_t c = c0; c < c1; ++c) seg += s_cnt[c * E + e];
+        // inclusive scan over the S segments of this expert (lanes e*S .. e*S + S - 1)
+        uint32_t inc = seg;
+        for (uint32_t dlt = 1; dlt < S; dlt <<= 1) {
+            const uint32_t o = __shfl_up(inc, dlt, S);
+            if (sg >= dlt) inc += o;
         }
-        s_tot[e] = run;
+        if (e < E) {
+            uint32_t run = inc - seg;
+            for (uint32_t c = c0; c < c1; ++c) {
+                const uint32_t t = s_cnt[c * E + e];
+                s_cnt[c * E + e] = run;
+                run += t;
+            }
+            if (sg == S - 1) s_tot[e] = inc;
+        }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t run = 0;
-        for (uint32_t e = 0; e < E; ++e) {
-            s_off[e] = run;
-            run += s_tot[e];
+    // expert offsets: exclusive scan of the totals by wave 0, eight experts a lane
+    if (wv == 0) {
+        uint32_t loc[8], sum = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t e = 8 * lane + i;
+            loc[i] = e < E ? s_tot[e] : 0u;
+            sum += loc[i];
         }
-        s_off[E] = run;
+        uint32_t inc = sum;
+        for (int dlt = 1; dlt < WAVE; dlt <<= 1) {
+            const uint32_t o = __shfl_up(inc, dlt);
+            if (lane >= dlt) inc += o;
+        }
+        uint32_t run = inc - sum;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t e = 8 * lane + i;
+            if (e <= E) s_off[e] = run;
+            run += loc[i];
+        }
+        if (lane == WAVE - 1) s_off[E] = inc;   // (E = 512 is past the last lane's eight)
     }
     __syncthreads();
     for (uint32_t e = threadIdx.x; e <= E; e += PERM_THREADS) offsets[e] = s_off[e];
-    // scatter: rank among equal ids of lower lanes of the same chunk
-    for (uint32_t c = wv; c < C; c += NW) {
+    // scatter: rank among equal ids of lower lanes of the same chunk; the
+    // lanes holding this lane's id are found bit by bit (one ballot per bit
+    // of an id below E)
+    uint32_t nbits = 1;
+    while ((1u << nbits) < E) ++nbits;
+    for (uint32_t cb = wv; cb < C; cb += NW * PERM_BATCH) {
+      if (!one_batch) load_ids(cb);
+#pragma unroll
+      for (int k = 0; k < PERM_BATCH; ++k) {
+        const uint32_t c = cb + k * NW;
+        if (c >= C) break;
         const uint32_t p = c * 64 + lane;
-        const uint32_t e = p < P ? ids[p] : 0xFFFFFFFFu;
+        const uint32_t e = eid[k];
         const bool ok = e < E;
-        uint32_t rank = 0;
-        for (uint64_t todo = __ballot(ok); todo != 0;) {
-            const uint32_t ev = readlane_u32(e, __builtin_ctzll(todo));
-            const uint64_t m = __ballot(ok && e == ev);
-            if (ok && e == ev) rank = __popcll(m & ((1ull << lane) - 1ull));
-            todo &= ~m;
+        uint64_t same = __ballot(ok);
+        for (uint32_t b = 0; b < nbits; ++b) {
+            const bool bit = (e >> b) & 1u;
+            const uint64_t set = __ballot(ok && bit);
+            same &= bit ? set : ~set;
         }
+        const uint32_t rank = __popcll(same & ((1ull << lane) - 1ull));
         if (ok) {
             const uint32_t dst = s_off[e] + s_cnt[c * E + e] + rank;
             sorted_pairs[dst] = p;
             if (sorted_tokens) sorted_tokens[dst] = p / K;
             if (sorted_w) sorted_w[dst] = w[p];
         }
+      }
     }
     // union order: touched experts ranked by first appearance
     if (union_ids) {
@@ -633,8 +692,20 @@ hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidde
 {
     if (d.E > SMOE_TOPK_MAX_N || d.K > SMOE_TOPK_MAX_K || d.D % 64 || T == 0) return hipErrorInvalidValue;
     const uint32_t cpl = (d.D / 32 + WAVE - 1) / WAVE;
-    if (cpl == 1) return route_c<1, 4>(d, L, hidden, T, normed, ids, w, s);
-    if (cpl == 2) return route_c<2, 2>(d, L, hidden, T, normed, ids, w, s);
+    // tokens per block: as many as keep one block per CU busy (each block
+    // reads the whole router matrix from L2 once), at most what the registers
+    // of a chunk per lane allow
+    const uint32_t cus = 256;
+    const uint32_t tb = T >= 4 * cus ? 4 : T >= 2 * cus ? 2 : 1;
+    if (cpl == 1) {
+        if (tb == 4) return route_c<1, 4>(d, L, hidden, T, normed, ids, w, s);
+        if (tb == 2) return route_c<1, 2>(d, L, hidden, T, normed, ids, w, s);
+        return route_c<1, 1>(d, L, hidden, T, normed, ids, w, s);
+    }
+    if (cpl == 2) {
+        if (tb >= 2) return route_c<2, 2>(d, L, hidden, T, normed, ids, w, s);
+        return route_c<2, 1>(d, L, hidden, T, normed, ids, w, s);
+    }
     if (cpl <= 4) return route_c<4, 1>(d, L, hidden, T, normed, ids, w, s);
     return hipErrorInvalidValue;
 }
