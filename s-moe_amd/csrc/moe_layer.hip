@@ -12,7 +12,8 @@
 //      words in XCD x's logit copy;
 //   2. softmax + top-k (scout.cpp:77-123) + renormalisation
 //      (decode.cpp:296-302) from that copy, in every wave;
-//   3. t < n_up: 8 rows of gate and up of expert ids[x] and
+//   3. t < n_up: RB rows (8, or 6 where that fills every wave) of gate and
+//      up of expert ids[x] and
 //      h = silu(gate) * up (kernels.metal:240-337), published in XCD x's
 //      h copy;
 //   4. t < n_down: RW rows of expert ids[x]'s down matrix (kernels.metal:
@@ -41,7 +42,7 @@ namespace smoe {
 namespace {
 
 constexpr uint32_t LX_SPIN_LIMIT = 1u << 22;
-constexpr int LX_UP_RB = 8;     // gate/up rows per wave
+constexpr int LX_UP_RB = 8;     // gate/up rows per wave (6 where that fills every wave)
 constexpr int LX_GROUP = 64;    // SMOE-Q4 group size (shatter_moe.py Q2_GROUP_SIZE)
 
 __device__ __forceinline__ uint64_t lx_word(float v, uint32_t tag)
@@ -72,13 +73,13 @@ __device__ __forceinline__ uint64_t get_agent(const uint64_t* p)
 
 }  // namespace
 
-template <int CPL, int VPL, int SEG, int DR>
+template <int CPL, int VPL, int SEG, int DR, int RB>
 __global__ __launch_bounds__(WAVE)
 void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* __restrict__ lx,
                  uint32_t* __restrict__ ids_out, float* __restrict__ w_out, uint32_t n_up, uint32_t n_down,
                  uint32_t* __restrict__ err)
 {
-    constexpr int RB = LX_UP_RB;
+    constexpr int NR = RB == 6 ? 16 : 2 * RB;   // reduced values (gate, up per row), padded to a power of two
     constexpr int GL = 1 << SEG;       // lanes of one down group
     constexpr int NG = WAVE / GL;      // down groups per wave
     constexpr int RW = NG * DR;        // down rows per wave
@@ -251,7 +252,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
         }
     };
 
-    // 3. gate/up rows 8t .. 8t + 7 of rank x -> h.  (Issuing the down loads
+    // 3. gate/up rows RB t .. RB t + RB - 1 of rank x -> h.  (Issuing the down loads
     //    any earlier than after this wave's up compute slows the launch:
     //    they compete with the gate/up stream every wave waits for.)
     if (t < n_up) {
@@ -276,7 +277,9 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        float part[2 * RB];
+        float part[NR];
+#pragma unroll
+        for (int i = 2 * RB; i < NR; ++i) part[i] = 0.f;
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
             float ga = 0.f, ua = 0.f;
@@ -288,8 +291,8 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
             part[2 * i] = ga;
             part[2 * i + 1] = ua;
         }
-        constexpr int USH = 6 - ilog2(2 * RB);
-        const float tot = wave_sum_rows<2 * RB>(part);
+        constexpr int USH = 6 - ilog2(NR);
+        const float tot = wave_sum_rows<NR>(part);
         const float gv = __shfl(tot, (2 * lane) << USH);
         const float uv = __shfl(tot, (2 * lane + 1) << USH);
         // silu(z) = z * (1 / (1 + exp(-z)))  (kernels.metal:61-63, :334-336)
@@ -400,18 +403,18 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
 namespace {
 
 struct LayerCfg {
-    int cpl, vpl, seg, dr;
+    int cpl, vpl, seg, dr, rb;
     uint32_t n_up, n_down, nbx;
 };
 
-template <int CPL, int VPL, int SEG, int DR>
+template <int CPL, int VPL, int SEG, int DR, int RB>
 uint32_t resident_blocks()
 {
     static uint32_t cap = [] {
         int dev = 0, per_cu = 0, cus = 0;
         if (hipGetDevice(&dev) != hipSuccess) return 0u;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0u;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_layer<CPL, VPL, SEG, DR>, WAVE, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_layer<CPL, VPL, SEG, DR, RB>, WAVE, 0) !=
             hipSuccess)
             return 0u;
         return static_cast<uint32_t>(per_cu) * static_cast<uint32_t>(cus);
@@ -437,21 +440,24 @@ bool layer_cfg(const MoeDims& d, LayerCfg& c)
     }
     const uint32_t rw = (64u >> c.seg) * c.dr;
     if (d.D % rw) return false;
-    c.n_up = d.I / LX_UP_RB;
     c.n_down = d.D / rw;
+    // 6 gate/up rows per wave where that gives every wave a row block: less
+    // dot-product work per wave than 8 rows on 3/4 of them
+    c.rb = (d.I % 6 == 0 && d.I / 6 == c.n_down) ? 6 : LX_UP_RB;
+    c.n_up = d.I / c.rb;
     c.nbx = std::max(c.n_up, c.n_down);
     // every wave produces a router row or a gate/up row block
     if (c.nbx > std::max(d.E, c.n_up)) return false;
     return true;
 }
 
-template <int CPL, int VPL, int SEG, int DR>
+template <int CPL, int VPL, int SEG, int DR, int RB>
 hipError_t launch_cfg(const LayerCfg& c, const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx,
                       uint32_t* ids, float* w, uint32_t* err, hipStream_t s, bool dry)
 {
-    if (8u * c.nbx > resident_blocks<CPL, VPL, SEG, DR>()) return hipErrorInvalidConfiguration;
+    if (8u * c.nbx > resident_blocks<CPL, VPL, SEG, DR, RB>()) return hipErrorInvalidConfiguration;
     if (dry) return hipSuccess;
-    launch_kernel(k_moe_layer<CPL, VPL, SEG, DR>, dim3(8u * c.nbx), dim3(WAVE), s, d, L, hidden, lx, ids, w, c.n_up,
+    launch_kernel(k_moe_layer<CPL, VPL, SEG, DR, RB>, dim3(8u * c.nbx), dim3(WAVE), s, d, L, hidden, lx, ids, w, c.n_up,
                   c.n_down, err);
     return hipGetLastError();
 }
@@ -462,8 +468,10 @@ hipError_t dispatch(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_
     LayerCfg c;
     if (!layer_cfg(d, c)) return hipErrorInvalidValue;
 #define SMOE_LAYER_CASE(C, V, S, R)                                                           \
-    if (c.cpl == C && c.vpl == V && c.seg == S && c.dr == R)                                  \
-        return launch_cfg<C, V, S, R>(c, d, L, hidden, lx, ids, w, err, s, dry);
+    if (c.cpl == C && c.vpl == V && c.seg == S && c.dr == R && c.rb == 8)                     \
+        return launch_cfg<C, V, S, R, 8>(c, d, L, hidden, lx, ids, w, err, s, dry);           \
+    if (c.cpl == C && c.vpl == V && c.seg == S && c.dr == R && c.rb == 6)                     \
+        return launch_cfg<C, V, S, R, 6>(c, d, L, hidden, lx, ids, w, err, s, dry);
     SMOE_LAYER_CASE(1, 2, 5, 8)
     SMOE_LAYER_CASE(1, 2, 6, 32)
     SMOE_LAYER_CASE(1, 8, 5, 8)
