@@ -50,7 +50,7 @@ void k_topk(const float* __restrict__ scores, uint32_t n, uint32_t k, uint32_t n
     topk_load<VPL>(scores + row * n, n, v);
     uint32_t my_id;
     float my_w;
-    const uint32_t count = topk_fast<VPL>(v, n, k, norm, my_id, my_w, slots);
+    const uint32_t count = topk_latency<VPL>(v, n, k, norm, my_id, my_w, slots);
     if (threadIdx.x < count) {
         ids[row * k + threadIdx.x] = my_id;
         w[row * k + threadIdx.x] = my_w;
@@ -249,7 +249,7 @@ __device__ __forceinline__ void moe_up_body(const MoeDims& d, const LayerDesc& L
     uint32_t my_id;
     float my_w;
     __shared__ uint2 slots[TOPK_SLOTS];
-    topk_fast<VPL>(v, d.E, d.K, d.norm_topk, my_id, my_w, slots);
+    topk_latency<VPL>(v, d.E, d.K, d.norm_topk, my_id, my_w, slots);
     const uint32_t expert = readlane_u32(my_id, r);
 
     if (b == 0 && static_cast<uint32_t>(lane) < d.K) {

@@ -222,7 +222,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
     uint32_t my_id;
     float my_w;
     __shared__ uint2 slots[TOPK_SLOTS];
-    topk_fast<VPL>(v, d.E, d.K, d.norm_topk, my_id, my_w, slots);
+    topk_latency<VPL>(v, d.E, d.K, d.norm_topk, my_id, my_w, slots);
     // (clamped: a timed-out exchange must still index inside the pool)
     const uint32_t expert = min(readlane_u32(my_id, static_cast<int>(x)), d.E - 1);
     if (x == 0 && t == 0 && static_cast<uint32_t>(lane) < d.K) {

@@ -404,7 +404,7 @@ void k_decode_stack(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_
             }
             uint32_t my_id;
             float my_w;
-            topk_fast<VPL>(v, E, K, d.norm_topk, my_id, my_w, topk_s[wv]);
+            topk_latency<VPL>(v, E, K, d.norm_topk, my_id, my_w, topk_s[wv]);
             if (x == 0 && jw == 0 && static_cast<uint32_t>(lane) < K) {
                 if (ids_out) ids_out[size_t(l) * K + lane] = my_id;
                 if (w_out) w_out[size_t(l) * K + lane] = my_w;

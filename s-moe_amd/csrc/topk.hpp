@@ -182,6 +182,192 @@ __device__ uint32_t topk_fast(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t 
     return count;
 }
 
+// ---------------------------------------------------------------------------
+// Softmax + top-k for n <= 128 scores (two positions per lane) and k <= 8,
+// by a sorting network instead of k serial rounds of max extraction.
+//
+// Selection runs on 32-bit keys that hold the score's order-preserving bits
+// with the low 7 replaced by 127 - position, so every key is distinct and
+// the network needs no tie-breaking.  Merging the lists of two lanes keeps
+// the top 8 of their union; after one merge per lane bit every lane holds
+// the top 8 keys in order.  The bit order is 5, 4 (v_permlane32/16_swap,
+// while the lists hold 2 and 4 keys and are merged whole by odd-even merges,
+// which compare equal indices only, so the swap's lane order does not
+// matter), then 3, 2, 1, 0 within rows (row_ror:8, row_half_mirror -- which
+// pairs quads that hold disjoint sets at that point -- and quad_perm), each
+// a bitonic top-8 merge.  The softmax (scout.cpp:85-98) runs beside the
+// network; it depends on the scores only.
+//
+// The keys only PROPOSE ranks.  The result stands when the probabilities of
+// the proposed ranks fall strictly, p_0 > ... > p_{c-1}, and the last is
+// strictly above every unselected probability: then each round of the
+// reference's selection with swaps (scout.cpp:101-110) has a strict unique
+// maximum and picks exactly rank s.  Otherwise (ties, probabilities equal
+// after rounding, scores equal in their top 25 bits and out of order, any
+// non-finite score) the row goes to topk_fast, which is exact everywhere.
+// Lane r < count receives (id_r, w_r) as from topk_fast; returns count.
+// ---------------------------------------------------------------------------
+constexpr int DPP_ROW_SHL1 = 0x101;
+
+__device__ __forceinline__ uint32_t order_bits(float f)
+{
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+// hi, lo <- max, min
+__device__ __forceinline__ void cmp_swap(uint32_t& hi, uint32_t& lo)
+{
+    const uint32_t a = hi;
+    hi = max(a, lo);
+    lo = min(a, lo);
+}
+// the two values of lane l and of lane l ^ 32 (BIT 5) or l ^ 16 (BIT 4), in an
+// order that depends on the lane
+template <int BIT>
+__device__ __forceinline__ void swap_pair(uint32_t v, uint32_t& x, uint32_t& y)
+{
+    const auto r = BIT == 5 ? __builtin_amdgcn_permlane32_swap(v, v, false, false)
+                            : __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    x = r[0];
+    y = r[1];
+}
+// a[j] of a list sorted in descending order, as the minimum of a[0..j] (a
+// select chain here is folded into an indexed load from scratch)
+__device__ __forceinline__ uint32_t sorted_at(const uint32_t (&a)[8], uint32_t j)
+{
+    uint32_t r = a[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) r = min(r, static_cast<uint32_t>(i) <= j ? a[i] : 0xFFFFFFFFu);
+    return r;
+}
+// top 8 of the union of this lane's sorted list and the partner's (DPP CTRL)
+template <int CTRL>
+__device__ __forceinline__ void merge8(uint32_t (&a)[8])
+{
+    uint32_t h[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = max(a[i], dpp_u32<CTRL>(0u, a[7 - i]));   // bitonic
+#pragma unroll
+    for (int d = 4; d >= 1; d >>= 1) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if ((i & d) == 0) cmp_swap(h[i], h[i + d]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = h[i];
+}
+
+template <int VPL>
+__device__ uint32_t topk_net(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t norm, uint32_t& my_id, float& my_w,
+                             uint2* slots)
+{
+    static_assert(VPL == 2, "topk_net holds two positions per lane");
+    const int lane = threadIdx.x & (WAVE - 1);
+    const uint32_t count = k < n ? k : n;
+    if (count != 0 && count <= 8 && n <= 128) {
+        // keys; a non-finite score fails the final check (the network's
+        // result is then unused)
+        uint32_t key[2];
+        bool bad = false;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t pos = lane + WAVE * j;
+            bad |= pos < n && !isfinite(v[j]);
+            key[j] = pos < n ? ((order_bits(v[j]) & ~127u) | (127u - pos)) : 0u;
+        }
+        // softmax, as topk_fast
+        float m = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            if (lane + WAVE * j < n) m = fmaxf(m, v[j]);
+        m = wave_max(m);
+        float e[2], sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            e[j] = lane + WAVE * j < n ? expf(v[j] - m) : 0.f;
+            sum += e[j];
+        }
+        sum = wave_sum(sum);
+        const float inv_sum = (sum > 0.f) ? 1.0f / sum : 0.f;
+
+        // lane bit 5: 2 + 2 keys
+        uint32_t a0 = max(key[0], key[1]), a1 = min(key[0], key[1]);
+        uint32_t c[8];
+        {
+            uint32_t x0, y0, x1, y1;
+            swap_pair<5>(a0, x0, y0);
+            swap_pair<5>(a1, x1, y1);
+            c[0] = max(x0, y0);
+            uint32_t mid0 = min(x0, y0), mid1 = max(x1, y1);
+            c[3] = min(x1, y1);
+            cmp_swap(mid1, mid0);
+            c[1] = mid1;
+            c[2] = mid0;
+        }
+        // lane bit 4: 4 + 4 keys, odd-even merge (evens, odds, then neighbours)
+        {
+            uint32_t x[4], y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) swap_pair<4>(c[i], x[i], y[i]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cmp_swap(x[i], y[i]);   // x = max, y = min of index i
+            // evens: {x0, y0} merged with {x2, y2}
+            uint32_t e0 = x[0], e1 = y[0], e2 = x[2], e3 = y[2];
+            cmp_swap(e1, e2);
+            // odds: {x1, y1} merged with {x3, y3}
+            uint32_t o0 = x[1], o1 = y[1], o2 = x[3], o3 = y[3];
+            cmp_swap(o1, o2);
+            c[0] = e0;
+            c[7] = o3;
+            cmp_swap(o0, e1);
+            cmp_swap(o1, e2);
+            cmp_swap(o2, e3);
+            c[1] = o0; c[2] = e1; c[3] = o1; c[4] = e2; c[5] = o2; c[6] = e3;
+        }
+        merge8<DPP_ROW_ROR8>(c);
+        merge8<DPP_ROW_HALF_MIRROR>(c);
+        merge8<DPP_QUAD_XOR2>(c);
+        merge8<DPP_QUAD_XOR1>(c);
+
+        // probabilities: of every position, of the proposed ranks (lane r),
+        // and the largest over the unselected positions
+        const uint32_t last = sorted_at(c, count - 1);
+        float p[2], rest = -1.f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            p[j] = e[j] * inv_sum;
+            if (lane + WAVE * j < n && key[j] < last) rest = fmaxf(rest, p[j]);
+        }
+        rest = wave_max(rest);
+        const uint32_t pos = 127u - (sorted_at(c, static_cast<uint32_t>(lane) & 7u) & 127u);
+        const float q0 = __shfl(p[0], static_cast<int>(pos & 63u));
+        const float q1 = __shfl(p[1], static_cast<int>(pos & 63u));
+        const float pr = static_cast<uint32_t>(lane) < count ? (pos >= 64u ? q1 : q0) : rest;
+        const float next = dpp_f32<DPP_ROW_SHL1>(-1.f, pr);   // lane r + 1's
+        if (__ballot(bad || (static_cast<uint32_t>(lane) < count && !(pr > next))) == 0) {
+            float ksum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)   // rank order, as the reference (x + 0 = x)
+                ksum += static_cast<uint32_t>(r) < count ? readlane_f32(pr, r) : 0.f;
+            my_id = static_cast<uint32_t>(lane) < count ? pos : 0u;
+            my_w = static_cast<uint32_t>(lane) < count ? pr : 0.f;
+            if (norm && ksum > 0.f) my_w = my_w * (1.0f / ksum);
+            return count;
+        }
+    }
+    return topk_fast<VPL>(v, n, k, norm, my_id, my_w, slots);
+}
+
+// The latency-bound callers (one row per wave on the critical path): the
+// network for up to 128 scores, max extraction above.
+template <int VPL>
+__device__ __forceinline__ uint32_t topk_latency(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t norm,
+                                                 uint32_t& my_id, float& my_w, uint2* slots)
+{
+    if constexpr (VPL == 2) return topk_net<VPL>(v, n, k, norm, my_id, my_w, slots);
+    else return topk_fast<VPL>(v, n, k, norm, my_id, my_w, slots);
+}
+
 // positions per lane for n experts: 2 (n <= 128) or 8 (n <= 512)
 static inline int topk_vpl(uint32_t n) { return n <= 128 ? 2 : 8; }
 
