@@ -463,7 +463,8 @@ __device__ __forceinline__ void grouped_mm_expert(
     GmW& w0, GmW& w1, GmW& w2, GmW& w3, GmA& a0, GmA& a1, GmA& a2, GmA& a3, uint32_t (&s_row)[GM_PASS],
     uint32_t (&s_pair)[GM_PASS])
 {
-    constexpr int AN = MS == 4 ? 2 : 1;          // activation loads per wave and stage (4 rows each)
+    constexpr int AN = MS >= 3 ? 2 : 1;          // activation loads per wave and stage (4 rows each;
+                                                 // at MS = 3 rows past the pass repeat its last row)
     constexpr int PASS = 16 * MS;
     const int lane = threadIdx.x & 63;
     const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -647,6 +648,9 @@ void k_grouped_mm(MoeDims d, LayerDesc L, const uint32_t* __restrict__ offsets,
                                       n_dim, k_dim, w0, w1, w2, w3, a0, a1, a2, a3, s_row, s_pair);
     else if (M <= 32)
         grouped_mm_expert<GATE_UP, 2>(d, L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, a_row_div, out,
+                                      n_dim, k_dim, w0, w1, w2, w3, a0, a1, a2, a3, s_row, s_pair);
+    else if (M <= 48)
+        grouped_mm_expert<GATE_UP, 3>(d, L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, a_row_div, out,
                                       n_dim, k_dim, w0, w1, w2, w3, a0, a1, a2, a3, s_row, s_pair);
     else
         grouped_mm_expert<GATE_UP, 4>(d, L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, a_row_div, out,
