@@ -11,15 +11,16 @@
 //   k_route        RMSNorm + fp32 router + exact top-k for TB tokens per
 //                  block; writes the normed rows (fp32) and ids/weights.
 //   k_split_rows   per row: power-of-two scale 2^e with |x| < 2^e and the
-//                  f16 hi/lo planes of x * 2^-e (hi + lo carries 22 bits).
+//                  f16 hi/lo planes of x * 2^-e (hi + lo carries 22 bits),
+//                  columns of every 8 in the order 0 2 4 6 1 3 5 7.
 //   k_permute      stable counting sort of the T*k (token, rank) pairs by
 //                  expert (one workgroup), union order by first appearance.
 //   k_grouped_mm   per expert: [tokens x K] x [K x 64 rows] tiles on MFMA
 //                  v_mfma_f32_16x16x32_f16, activation chunks staged in LDS.
-//                  Weights enter exactly as 2c - 15 (f16), activations as hi
-//                  and lo planes (two MFMAs into one fp32 accumulator); each
-//                  64-column group adds s_g * sum, the row scale 2^e / 15
-//                  closes the dot (kernels.metal:90-105, 140-145).  Gate+up
+//                  Weights enter exactly as (2c - 15)/8 (f16), activations as
+//                  hi and lo planes (two MFMAs into one fp32 accumulator);
+//                  each 64-column group adds s_g * sum, the row scale
+//                  8 * 2^e / 15 closes the dot (kernels.metal:90-105, 140-145).  Gate+up
 //                  runs with SiLU and writes h per (token, rank) pair; down
 //                  writes y per pair.
 //   k_combine_pairs hidden[t] += sum_r w[t][r] * y[t*k + r] in rank order.
@@ -175,7 +176,10 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
 // k_split_rows: src [rows x cols] fp32 -> f16 planes hi/lo of x * 2^-e with
 // |x| < 2^e over the row, and scale[row] = 2^e.  hi + lo carries 22 bits of
 // x * 2^-e (f16 subnormals below 2^-14 still hold x to 2^-25 of the row max).
-// One wave per row.
+// Within every 8 columns the planes hold the columns in the order
+// 0 2 4 6 1 3 5 7, the order in which q4_codes_to_f16 unpacks a word of
+// codes (the even codes, then the odd ones).  One wave per row, 8 columns
+// per lane.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256)
 void k_split_rows(const float* __restrict__ src, uint32_t rows, uint32_t cols, uint16_t* __restrict__ hi,
@@ -191,20 +195,27 @@ void k_split_rows(const float* __restrict__ src, uint32_t rows, uint32_t cols, u
         }
         amax = wave_max(amax);
         const int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
-        for (uint32_t c = lane * 4; c < cols; c += WAVE * 4) {
-            const float4 v = load_f4(x + c);
-            const float xs[4] = {__builtin_ldexpf(v.x, -e), __builtin_ldexpf(v.y, -e), __builtin_ldexpf(v.z, -e),
-                                 __builtin_ldexpf(v.w, -e)};
-            uint16_t h4[4], l4[4];
+        for (uint32_t c = lane * 8; c < cols; c += WAVE * 8) {
+            const float4 v0 = load_f4(x + c), v1 = load_f4(x + c + 4);
+            // stored order: columns 0 2 4 6 1 3 5 7 of the 8
+            const float xs[8] = {v0.x, v0.z, v1.x, v1.z, v0.y, v0.w, v1.y, v1.w};
+            uint32_t h2[4], l2[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const _Float16 h = static_cast<_Float16>(xs[i]);
-                h4[i] = __builtin_bit_cast(uint16_t, h);
-                l4[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(xs[i] - static_cast<float>(h)));
+                uint32_t hb[2], lb[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const float xv = __builtin_ldexpf(xs[2 * i + u], -e);
+                    const _Float16 h = static_cast<_Float16>(xv);
+                    hb[u] = __builtin_bit_cast(uint16_t, h);
+                    lb[u] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(xv - static_cast<float>(h)));
+                }
+                h2[i] = hb[0] | (hb[1] << 16);
+                l2[i] = lb[0] | (lb[1] << 16);
             }
             const size_t o = static_cast<size_t>(r) * cols + c;
-            *reinterpret_cast<uint2*>(hi + o) = make_uint2(h4[0] | (uint32_t(h4[1]) << 16), h4[2] | (uint32_t(h4[3]) << 16));
-            *reinterpret_cast<uint2*>(lo + o) = make_uint2(l4[0] | (uint32_t(l4[1]) << 16), l4[2] | (uint32_t(l4[3]) << 16));
+            *reinterpret_cast<uint4*>(hi + o) = make_uint4(h2[0], h2[1], h2[2], h2[3]);
+            *reinterpret_cast<uint4*>(lo + o) = make_uint4(l2[0], l2[1], l2[2], l2[3]);
         }
         if (lane == 0) scale[r] = __builtin_ldexpf(1.0f, e);
     }
@@ -394,8 +405,9 @@ void k_permute(const uint32_t* __restrict__ ids, const float* __restrict__ w, ui
 // v_mfma_f32_16x16x32_f16 operand layout: lane l holds A[l % 16][8 (l/16) + j]
 // and B[8 (l/16) + j][l % 16] (j < 8) and receives D[4 (l/16) + i][l % 16].
 // Inside a 64-column group, lane quarter q = l/16 of MFMA step s uses the
-// physical columns 16 q + 8 s + j.  Weights enter as f16 (2c - 15) (exact), so
-// a group's MFMA sum times s_g is 15/7.5 of its dequantised dot product
+// physical columns 16 q + 8 s + j (both operands hold a lane's 8 columns in
+// the order 0 2 4 6 1 3 5 7).  Weights enter as f16 (2c - 15)/8 (exact), so
+// a group's MFMA sum times s_g is 15/60 of its dequantised dot product
 // (kernels.metal:90-105, 140-145) and the epilogue is one FMA per output.
 // LDS layouts (16-byte slots; XOR swizzles keep the fragment reads free of
 // bank conflicts):
@@ -419,16 +431,21 @@ struct GmA { uint8_t a[GM_PASS * 256]; };    // one activation stage: row = 16 s
 
 #define SMOE_LDS_AS(p) ((__attribute__((address_space(3))) void*)(p))
 
+// 8 codes (a word: byte b holds codes 2b (low nibble) and 2b + 1) -> 8 f16
+// (c - 7.5) / 4 in the order 0 2 4 6 1 3 5 7.  A code shifted to bits 4..7 of
+// a byte under the byte 0x4C is the f16 16 + c/4 (exponent 4, mantissa
+// c << 4), one v_perm per two codes; 16 + c/4 - 17.875 = (c - 7.5)/4 is exact.
 __device__ __forceinline__ half8_t q4_codes_to_f16(uint32_t v)
 {
-    const uint32_t E = v & 0x0F0F0F0Fu;
-    const uint32_t O = (v >> 4) & 0x0F0F0F0Fu;
+    const uint32_t E = (v << 4) & 0xF0F0F0F0u;    // even codes << 4
+    const uint32_t O = v & 0xF0F0F0F0u;           // odd codes << 4
+    const uint32_t K = 0x4C4C4C4Cu;
     u32x4_t r;
-    r.x = (__builtin_amdgcn_perm(O, E, 0x0C040C00u) << 1) | 0x64006400u;
-    r.y = (__builtin_amdgcn_perm(O, E, 0x0C050C01u) << 1) | 0x64006400u;
-    r.z = (__builtin_amdgcn_perm(O, E, 0x0C060C02u) << 1) | 0x64006400u;
-    r.w = (__builtin_amdgcn_perm(O, E, 0x0C070C03u) << 1) | 0x64006400u;
-    const _Float16 b = static_cast<_Float16>(-1039.0f);
+    r.x = __builtin_amdgcn_perm(K, E, 0x04010400u);   // codes 0, 2
+    r.y = __builtin_amdgcn_perm(K, E, 0x04030402u);   // codes 4, 6
+    r.z = __builtin_amdgcn_perm(K, O, 0x04010400u);   // codes 1, 3
+    r.w = __builtin_amdgcn_perm(K, O, 0x04030402u);   // codes 5, 7
+    const _Float16 b = static_cast<_Float16>(-17.875f);
     const half8_t bias = {b, b, b, b, b, b, b, b};
     return __builtin_bit_cast(half8_t, r) + bias;
 }
@@ -607,7 +624,7 @@ __device__ __forceinline__ void grouped_mm_expert(
             for (int i = 0; i < 4; ++i) {
                 const uint32_t m = 16 * ms + 4 * q + i;
                 if (m0 + m >= M) continue;
-                const float rs = a_scale[s_row[m]] * (1.0f / 15.0f);
+                const float rs = a_scale[s_row[m]] * (8.0f / 15.0f);   // weights are (2c - 15) / 8
                 float* o = out + static_cast<size_t>(s_pair[m]) * n_dim;
                 if (GATE_UP) {
                     const uint32_t n = tile * GM_ROWS_GU + 16 * wv + m16;
