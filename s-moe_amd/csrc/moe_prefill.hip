@@ -682,15 +682,22 @@ __global__ __launch_bounds__(256)
 void k_combine_pairs(const float* __restrict__ y, const float* __restrict__ w, uint32_t K, uint32_t D,
                      float* __restrict__ hidden)
 {
-    const uint32_t t = blockIdx.y, col = blockIdx.x * 256 + threadIdx.x;
+    // 4 columns per thread; the K rank rows of token t are K float4 loads in flight
+    const uint32_t t = blockIdx.y, col = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (col >= D) return;
-    float acc = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (uint32_t r = 0; r < K; ++r) {
         const size_t p = static_cast<size_t>(t) * K + r;
-        acc = fmaf(w[p], y[p * D + col], acc);
+        const float wr = w[p];
+        const float4 v = load_f4(y + p * D + col);
+        acc.x = fmaf(wr, v.x, acc.x);
+        acc.y = fmaf(wr, v.y, acc.y);
+        acc.z = fmaf(wr, v.z, acc.z);
+        acc.w = fmaf(wr, v.w, acc.w);
     }
-    float* h = hidden + static_cast<size_t>(t) * D + col;
-    *h = *h + acc;
+    float4* h = reinterpret_cast<float4*>(hidden + static_cast<size_t>(t) * D + col);
+    const float4 o = *h;
+    *h = make_float4(o.x + acc.x, o.y + acc.y, o.z + acc.z, o.w + acc.w);
 }
 
 // ---------------------------------------------------------------------------
@@ -782,7 +789,8 @@ hipError_t launch_grouped_down(const MoeDims& d, const LayerDesc& L, const uint3
 hipError_t launch_combine_pairs(const float* y, const float* w, uint32_t T, uint32_t K, uint32_t D, float* hidden,
                                 hipStream_t s)
 {
-    launch_kernel(k_combine_pairs, dim3((D + 255) / 256, T), dim3(256), s, y, w, K, D, hidden);
+    if (D % 4) return hipErrorInvalidValue;
+    launch_kernel(k_combine_pairs, dim3((D / 4 + 255) / 256, T), dim3(256), s, y, w, K, D, hidden);
     return hipGetLastError();
 }
 
