@@ -44,6 +44,8 @@ struct PrefillScratch {
     uint16_t* x_hi = nullptr;       // [T x D] f16
     uint16_t* x_lo = nullptr;
     float* x_sc = nullptr;          // [T] row scales
+    float* logits = nullptr;        // [T x E] router logits (short batches)
+    uint32_t* rt_ctr = nullptr;     // [T] route counters (zero between launches)
     uint32_t* ids = nullptr;        // [T x K]
     float* w = nullptr;             // [T x K]
     uint32_t* offsets = nullptr;    // [E + 1]
@@ -158,6 +160,8 @@ void free_prefill_scratch(PrefillScratch& s)
     dfree(s.x_hi);
     dfree(s.x_lo);
     dfree(s.x_sc);
+    dfree(s.logits);
+    dfree(s.rt_ctr);
     dfree(s.ids);
     dfree(s.w);
     dfree(s.offsets);
@@ -291,7 +295,9 @@ int ensure_prefill_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
                     dalloc(ctx, &n.x_lo, T_ * n.D) && dalloc(ctx, &n.x_sc, T_) &&
                     dalloc(ctx, &n.ids, P) && dalloc(ctx, &n.w, P) && dalloc(ctx, &n.offsets, size_t(n.E) + 1) &&
                     dalloc(ctx, &n.pairs, P) && dalloc(ctx, &n.h, P * n.I) && dalloc(ctx, &n.h_hi, P * n.I) &&
-                    dalloc(ctx, &n.h_lo, P * n.I) && dalloc(ctx, &n.h_sc, P) && dalloc(ctx, &n.y, P * n.D);
+                    dalloc(ctx, &n.h_lo, P * n.I) && dalloc(ctx, &n.h_sc, P) && dalloc(ctx, &n.y, P * n.D) &&
+                    dalloc(ctx, &n.logits, T_ * n.E) && dalloc(ctx, &n.rt_ctr, T_) &&
+                    hip_ok(ctx, hipMemset(n.rt_ctr, 0, T_ * sizeof(uint32_t)), "hipMemset");
     if (!ok) {
         free_prefill_scratch(n);
         return SMOE_ERR_HIP;
@@ -909,7 +915,7 @@ extern "C" int smoe_hip_moe_prefill(SmoeMetalCtx* ctx, const SmoeMoeShape* shape
         float* w = weights_out ? weights_out + size_t(t0) * d.K : s.w;
         uint32_t* offs = expert_offsets ? expert_offsets : s.offsets;
         if (!timed(ctx, SMOE_KERNEL_ROUTE, "route",
-                   [&] { return smoe::launch_route(d, L, hv, T, s.normed, ids, w, st); }) ||
+                   [&] { return smoe::launch_route(d, L, hv, T, s.normed, ids, w, s.logits, s.rt_ctr, st); }) ||
             !timed(ctx, SMOE_KERNEL_SPLIT, "split(x)",
                    [&] { return smoe::launch_split_rows(s.normed, T, d.D, s.x_hi, s.x_lo, s.x_sc, st); }) ||
             !timed(ctx, SMOE_KERNEL_PERMUTE, "permute", [&] {

@@ -46,20 +46,31 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 // softmax/top-k (scout.cpp:77-123) for TB tokens per block of ROUTE_WAVES
 // waves.  Every wave normalises all TB tokens (lane l owns the 32-column
 // chunks l + 64 j) and computes router rows w, w + ROUTE_WAVES, ... for all of
-// them; wave t then selects the experts of token t.
+// them; wave t then selects the experts of token t.  With ES > 1 (short
+// batches) the E router rows of a token group are split over ES blocks, so
+// each wave has few rows and all their loads in flight at once: the blocks
+// write their logits to memory, count themselves on a device-scope counter
+// per token group, and the last one (count = ES - 1 modulo ES) runs the
+// group's top-k.
 // ---------------------------------------------------------------------------
 constexpr int ROUTE_WAVES = 8;
 
-template <int CPL, int TB, int VPL>
+template <int CPL, int TB, int VPL, int ES>
 __global__ __launch_bounds__(ROUTE_WAVES * WAVE)
 void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t T, float* __restrict__ normed,
-             uint32_t* __restrict__ ids, float* __restrict__ w)
+             uint32_t* __restrict__ ids, float* __restrict__ w, float* __restrict__ logits,
+             uint32_t* __restrict__ counters)
 {
-    constexpr int RPB = 16 / TB;   // router rows per reduction batch (RPB * TB values)
+    // router rows per reduction batch (RPB * TB values); with ES > 1 a wave
+    // has at most 4 rows (E <= 128 at ES = 4)
+    constexpr int RPB = ES > 1 ? 4 : 16 / TB;
     __shared__ float s_logit[TB][SMOE_TOPK_MAX_N];
     __shared__ uint2 s_slots[TB][TOPK_SLOTS];
+    __shared__ uint32_t s_last;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const uint32_t t0 = blockIdx.x * TB;
+    const uint32_t g = blockIdx.x / ES, eg = blockIdx.x % ES;
+    const uint32_t t0 = g * TB;
+    const uint32_t rows_per = (d.E + ES - 1) / ES, rbeg = eg * rows_per, rend = min(d.E, rbeg + rows_per);
     const uint32_t D = d.D, nch = D >> 5;
 
     float a[TB][CPL][32];
@@ -103,8 +114,8 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
                 a[t][j][4 * q + 3] = (x[j][q].w * inv) * bf16_to_f32(g1 >> 16);
             }
         }
-        // wave t stores token t's normed row
-        if (wv == t && t0 + t < T) {
+        // wave t of the group's first block stores token t's normed row
+        if (wv == t && eg == 0 && t0 + t < T) {
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 if (lane + WAVE * j < nch) {
@@ -117,13 +128,13 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
             }
         }
     }
-    // router rows of this wave, RPB at a time; lane l ends up with value l >> 2
-    // of the batch (value v = row_i * TB + t)
-    for (uint32_t r0 = wv * RPB; r0 < d.E; r0 += ROUTE_WAVES * RPB) {
+    // router rows of this wave, RPB at a time; lane l ends up with value
+    // l >> VSH of the batch (value v = row_i * TB + t)
+    for (uint32_t r0 = rbeg + wv * RPB; r0 < rend; r0 += ROUTE_WAVES * RPB) {
         float part[RPB * TB];
 #pragma unroll
         for (int i = 0; i < RPB; ++i) {
-            const uint16_t* wr = L.router_w + static_cast<size_t>(min(r0 + i, d.E - 1)) * D;
+            const uint16_t* wr = L.router_w + static_cast<size_t>(min(r0 + i, rend - 1)) * D;
             uint4 rw[CPL][4];
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
@@ -150,17 +161,40 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
             }
         }
         const float tot = wave_sum_rows<RPB * TB>(part);
-        const uint32_t v = lane >> 2;
+        constexpr int VSH = 6 - ilog2(RPB * TB);   // lane l holds the total of value l >> VSH
+        const uint32_t v = lane >> VSH;
         const uint32_t row = r0 + v / TB;
-        if ((lane & 3) == 0 && row < d.E && row < r0 + RPB) s_logit[v % TB][row] = tot;
+        if ((lane & ((1 << VSH) - 1)) == 0 && row < rend && row < r0 + RPB) {
+            if (ES == 1) s_logit[v % TB][row] = tot;
+            else if (t0 + v % TB < T)   // written through to the agent's coherence point
+                __hip_atomic_store(&logits[static_cast<size_t>(t0 + v % TB) * d.E + row], tot, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
-    __syncthreads();
+    if (ES > 1) {
+        // every wave's agent-scope stores complete before the block counts
+        // itself (no device-wide fence: that writes back and invalidates the
+        // whole L2 of the XCD)
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        asm volatile("" ::: "memory");
+        __syncthreads();
+        // the count is kept modulo ES (ES divides 2^32): no reset between launches
+        if (threadIdx.x == 0) s_last = atomicAdd(&counters[g], 1u) % ES == ES - 1;
+        __syncthreads();
+        if (!s_last) return;
+    } else {
+        __syncthreads();
+    }
     if (wv < TB && t0 + wv < T) {
         float p[VPL];
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
             const uint32_t pos = lane + WAVE * j;
-            p[j] = pos < d.E ? s_logit[wv][pos] : -INFINITY;
+            p[j] = pos >= d.E ? -INFINITY
+                   : ES == 1  ? s_logit[wv][pos]
+                              : __hip_atomic_load(&logits[static_cast<size_t>(t0 + wv) * d.E + pos],
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         uint32_t my_id;
         float my_w;
@@ -703,38 +737,42 @@ void k_combine_pairs(const float* __restrict__ y, const float* __restrict__ w, u
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-template <int CPL, int TB>
+template <int CPL, int TB, int ES = 1>
 static hipError_t route_c(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, float* normed,
-                          uint32_t* ids, float* w, hipStream_t s)
+                          uint32_t* ids, float* w, float* logits, uint32_t* counters, hipStream_t s)
 {
-    const dim3 grid((T + TB - 1) / TB), block(ROUTE_WAVES * WAVE);
+    const dim3 grid(((T + TB - 1) / TB) * ES), block(ROUTE_WAVES * WAVE);
     if (d.E <= 128)
-        launch_kernel(k_route<CPL, TB, 2>, grid, block, s, d, L, hidden, T, normed, ids, w);
+        launch_kernel(k_route<CPL, TB, 2, ES>, grid, block, s, d, L, hidden, T, normed, ids, w, logits, counters);
     else
-        launch_kernel(k_route<CPL, TB, 8>, grid, block, s, d, L, hidden, T, normed, ids, w);
+        launch_kernel(k_route<CPL, TB, 8, ES>, grid, block, s, d, L, hidden, T, normed, ids, w, logits, counters);
     return hipGetLastError();
 }
 
 hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, float* normed,
-                        uint32_t* ids, float* w, hipStream_t s)
+                        uint32_t* ids, float* w, float* logits, uint32_t* counters, hipStream_t s)
 {
     if (d.E > SMOE_TOPK_MAX_N || d.K > SMOE_TOPK_MAX_K || d.D % 64 || T == 0) return hipErrorInvalidValue;
     const uint32_t cpl = (d.D / 32 + WAVE - 1) / WAVE;
     // tokens per block: as many as keep one block per CU busy (each block
     // reads the whole router matrix from L2 once), at most what the registers
-    // of a chunk per lane allow
+    // of a chunk per lane allow.  Under 128 tokens (one per block) the router
+    // rows of a token are split over 4 blocks (needs E <= 128: 4 rows a wave).
     const uint32_t cus = 256;
     const uint32_t tb = T >= 4 * cus ? 4 : T >= 2 * cus ? 2 : 1;
+    const bool split = T < 128 && d.E <= 128 && logits && counters;
     if (cpl == 1) {
-        if (tb == 4) return route_c<1, 4>(d, L, hidden, T, normed, ids, w, s);
-        if (tb == 2) return route_c<1, 2>(d, L, hidden, T, normed, ids, w, s);
-        return route_c<1, 1>(d, L, hidden, T, normed, ids, w, s);
+        if (tb == 4) return route_c<1, 4>(d, L, hidden, T, normed, ids, w, logits, counters, s);
+        if (tb == 2) return route_c<1, 2>(d, L, hidden, T, normed, ids, w, logits, counters, s);
+        if (split) return route_c<1, 1, 4>(d, L, hidden, T, normed, ids, w, logits, counters, s);
+        return route_c<1, 1>(d, L, hidden, T, normed, ids, w, logits, counters, s);
     }
     if (cpl == 2) {
-        if (tb >= 2) return route_c<2, 2>(d, L, hidden, T, normed, ids, w, s);
-        return route_c<2, 1>(d, L, hidden, T, normed, ids, w, s);
+        if (tb >= 2) return route_c<2, 2>(d, L, hidden, T, normed, ids, w, logits, counters, s);
+        if (split) return route_c<2, 1, 4>(d, L, hidden, T, normed, ids, w, logits, counters, s);
+        return route_c<2, 1>(d, L, hidden, T, normed, ids, w, logits, counters, s);
     }
-    if (cpl <= 4) return route_c<4, 1>(d, L, hidden, T, normed, ids, w, s);
+    if (cpl <= 4) return route_c<4, 1>(d, L, hidden, T, normed, ids, w, logits, counters, s);
     return hipErrorInvalidValue;
 }
 
