@@ -40,7 +40,6 @@ struct DeviceScratch {
 // prefill / permute scratch for one batch of up to T tokens (P = T * K pairs)
 struct PrefillScratch {
     uint32_t D = 0, E = 0, K = 0, I = 0, T = 0;
-    float* normed = nullptr;        // [T x D]
     uint16_t* x_hi = nullptr;       // [T x D] f16
     uint16_t* x_lo = nullptr;
     float* x_sc = nullptr;          // [T] row scales
@@ -156,7 +155,6 @@ void free_device_scratch(DeviceScratch& s)
 
 void free_prefill_scratch(PrefillScratch& s)
 {
-    dfree(s.normed);
     dfree(s.x_hi);
     dfree(s.x_lo);
     dfree(s.x_sc);
@@ -279,7 +277,7 @@ uint32_t prefill_max_tokens(uint32_t E, uint32_t K)
 int ensure_prefill_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
 {
     PrefillScratch& c = ctx->ps;
-    if (c.normed && c.D >= s->d_model && c.E >= s->n_experts && c.K >= s->top_k && c.I >= s->d_ff && c.T >= T)
+    if (c.x_hi && c.D >= s->d_model && c.E >= s->n_experts && c.K >= s->top_k && c.I >= s->d_ff && c.T >= T)
         return SMOE_OK;
     if (stream_capturing(ctx->stream)) return SMOE_ERR_CAPTURE;
     if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
@@ -291,7 +289,7 @@ int ensure_prefill_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
     n.T = std::max(c.T, T);
     free_prefill_scratch(c);
     const size_t T_ = n.T, P = T_ * n.K;
-    const bool ok = dalloc(ctx, &n.normed, T_ * n.D) && dalloc(ctx, &n.x_hi, T_ * n.D) &&
+    const bool ok = dalloc(ctx, &n.x_hi, T_ * n.D) &&
                     dalloc(ctx, &n.x_lo, T_ * n.D) && dalloc(ctx, &n.x_sc, T_) &&
                     dalloc(ctx, &n.ids, P) && dalloc(ctx, &n.w, P) && dalloc(ctx, &n.offsets, size_t(n.E) + 1) &&
                     dalloc(ctx, &n.pairs, P) && dalloc(ctx, &n.h, P * n.I) && dalloc(ctx, &n.h_hi, P * n.I) &&
@@ -915,9 +913,9 @@ extern "C" int smoe_hip_moe_prefill(SmoeMetalCtx* ctx, const SmoeMoeShape* shape
         float* w = weights_out ? weights_out + size_t(t0) * d.K : s.w;
         uint32_t* offs = expert_offsets ? expert_offsets : s.offsets;
         if (!timed(ctx, SMOE_KERNEL_ROUTE, "route",
-                   [&] { return smoe::launch_route(d, L, hv, T, s.normed, ids, w, s.logits, s.rt_ctr, st); }) ||
-            !timed(ctx, SMOE_KERNEL_SPLIT, "split(x)",
-                   [&] { return smoe::launch_split_rows(s.normed, T, d.D, s.x_hi, s.x_lo, s.x_sc, st); }) ||
+                   [&] {
+                       return smoe::launch_route(d, L, hv, T, s.x_hi, s.x_lo, s.x_sc, ids, w, s.logits, s.rt_ctr, st);
+                   }) ||
             !timed(ctx, SMOE_KERNEL_PERMUTE, "permute", [&] {
                 return smoe::launch_permute(ids, w, P, d.K, d.E, offs, s.pairs, sorted_tokens, nullptr, union_ids,
                                             union_size, ctx->d_err, st);

@@ -174,12 +174,14 @@ hipError_t launch_attention(const AttnDims& a, const float* q, const float* k, c
                             void* scratch, float* attn_out, hipStream_t s);
 
 // ---- prefill, T token rows (moe_prefill.hip) -----------------------------
-// RMSNorm + router + top-k for T tokens: normed [T x D], ids/w [T x K].
-// logits [T x E] and counters [T] (zero at allocation; every launch adds a
-// multiple of 4) serve the short-batch form; with either null every token
-// group runs in one block.
-hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, float* normed,
-                        uint32_t* ids, float* w, float* logits, uint32_t* counters, hipStream_t s);
+// RMSNorm + router + top-k for T tokens: the normed rows as f16 planes
+// x_hi/x_lo [T x D] with row scales x_sc [T] (as launch_split_rows writes
+// them), ids/w [T x K].  logits [T x E] and counters [T] (zero at allocation;
+// every launch adds a multiple of 4) serve the short-batch form; with either
+// null every token group runs in one block.
+hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, uint16_t* x_hi,
+                        uint16_t* x_lo, float* x_sc, uint32_t* ids, float* w, float* logits, uint32_t* counters,
+                        hipStream_t s);
 // Per row of src [rows x cols]: f16 hi/lo planes of x * 2^-e (|x| < 2^e over
 // the row) and scale[row] = 2^e.
 hipError_t launch_split_rows(const float* src, uint32_t rows, uint32_t cols, uint16_t* hi, uint16_t* lo,

@@ -9,7 +9,8 @@
 // changes fp32 summation order):
 //
 //   k_route        RMSNorm + fp32 router + exact top-k for TB tokens per
-//                  block; writes the normed rows (fp32) and ids/weights.
+//                  block; writes the normed rows as the GEMM's f16 planes
+//                  (the split below) and ids/weights.
 //   k_split_rows   per row: power-of-two scale 2^e with |x| < 2^e and the
 //                  f16 hi/lo planes of x * 2^-e (hi + lo carries 22 bits),
 //                  columns of every 8 in the order 0 2 4 6 1 3 5 7.
@@ -42,6 +43,32 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
+// 8 consecutive columns x[0..7] of a row with |x| < 2^e -> f16 planes hi, lo of
+// x * 2^-e (hi + lo carries 22 bits), in the column order 0 2 4 6 1 3 5 7 in
+// which q4_codes_to_f16 unpacks a word of codes.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void split8_f16(const float* x, int e, uint4& hi, uint4& lo)
+{
+    const float xs[8] = {x[0], x[2], x[4], x[6], x[1], x[3], x[5], x[7]};
+    uint32_t h2[4], l2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t hb[2], lb[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const float xv = __builtin_ldexpf(xs[2 * i + u], -e);
+            const _Float16 h = static_cast<_Float16>(xv);
+            hb[u] = __builtin_bit_cast(uint16_t, h);
+            lb[u] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(xv - static_cast<float>(h)));
+        }
+        h2[i] = hb[0] | (hb[1] << 16);
+        l2[i] = lb[0] | (lb[1] << 16);
+    }
+    hi = make_uint4(h2[0], h2[1], h2[2], h2[3]);
+    lo = make_uint4(l2[0], l2[1], l2[2], l2[3]);
+}
+
+// ---------------------------------------------------------------------------
 // k_route: RMSNorm (common.hpp:245-256) + router (common.hpp:293-306) +
 // softmax/top-k (scout.cpp:77-123) for TB tokens per block of ROUTE_WAVES
 // waves.  Every wave normalises all TB tokens (lane l owns the 32-column
@@ -57,9 +84,9 @@ constexpr int ROUTE_WAVES = 8;
 
 template <int CPL, int TB, int VPL, int ES>
 __global__ __launch_bounds__(ROUTE_WAVES * WAVE)
-void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t T, float* __restrict__ normed,
-             uint32_t* __restrict__ ids, float* __restrict__ w, float* __restrict__ logits,
-             uint32_t* __restrict__ counters)
+void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t T, uint16_t* __restrict__ x_hi,
+             uint16_t* __restrict__ x_lo, float* __restrict__ x_sc, uint32_t* __restrict__ ids,
+             float* __restrict__ w, float* __restrict__ logits, uint32_t* __restrict__ counters)
 {
     // router rows per reduction batch (RPB * TB values); with ES > 1 a wave
     // has at most 4 rows (E <= 128 at ES = 4)
@@ -114,18 +141,32 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
                 a[t][j][4 * q + 3] = (x[j][q].w * inv) * bf16_to_f32(g1 >> 16);
             }
         }
-        // wave t of the group's first block stores token t's normed row
+        // wave t of the group's first block writes token t's normed row as the
+        // grouped GEMM's f16 planes (the split of k_split_rows, same values)
         if (wv == t && eg == 0 && t0 + t < T) {
+            float amax = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                if (lane + WAVE * j < nch) {
+#pragma unroll
+                    for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(a[t][j][k]));
+                }
+            amax = wave_max(amax);
+            const int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
+            const size_t row = static_cast<size_t>(t0 + t) * D;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
-                if (lane + WAVE * j < nch) {
-                    float* o = normed + static_cast<size_t>(t0 + t) * D + (lane + WAVE * j) * 32;
+                if (lane + WAVE * j >= nch) continue;
 #pragma unroll
-                    for (int q = 0; q < 8; ++q)
-                        *reinterpret_cast<float4*>(o + 4 * q) =
-                            make_float4(a[t][j][4 * q], a[t][j][4 * q + 1], a[t][j][4 * q + 2], a[t][j][4 * q + 3]);
+                for (int b = 0; b < 4; ++b) {
+                    const size_t o = row + (lane + WAVE * j) * 32 + 8 * b;
+                    uint4 hv, lv;
+                    split8_f16(&a[t][j][8 * b], e, hv, lv);
+                    *reinterpret_cast<uint4*>(x_hi + o) = hv;
+                    *reinterpret_cast<uint4*>(x_lo + o) = lv;
                 }
             }
+            if (lane == 0) x_sc[t0 + t] = __builtin_ldexpf(1.0f, e);
         }
     }
     // router rows of this wave, RPB at a time; lane l ends up with value
@@ -231,25 +272,12 @@ void k_split_rows(const float* __restrict__ src, uint32_t rows, uint32_t cols, u
         const int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
         for (uint32_t c = lane * 8; c < cols; c += WAVE * 8) {
             const float4 v0 = load_f4(x + c), v1 = load_f4(x + c + 4);
-            // stored order: columns 0 2 4 6 1 3 5 7 of the 8
-            const float xs[8] = {v0.x, v0.z, v1.x, v1.z, v0.y, v0.w, v1.y, v1.w};
-            uint32_t h2[4], l2[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t hb[2], lb[2];
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const float xv = __builtin_ldexpf(xs[2 * i + u], -e);
-                    const _Float16 h = static_cast<_Float16>(xv);
-                    hb[u] = __builtin_bit_cast(uint16_t, h);
-                    lb[u] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(xv - static_cast<float>(h)));
-                }
-                h2[i] = hb[0] | (hb[1] << 16);
-                l2[i] = lb[0] | (lb[1] << 16);
-            }
+            const float xv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            uint4 hv, lv;
+            split8_f16(xv, e, hv, lv);
             const size_t o = static_cast<size_t>(r) * cols + c;
-            *reinterpret_cast<uint4*>(hi + o) = make_uint4(h2[0], h2[1], h2[2], h2[3]);
-            *reinterpret_cast<uint4*>(lo + o) = make_uint4(l2[0], l2[1], l2[2], l2[3]);
+            *reinterpret_cast<uint4*>(hi + o) = hv;
+            *reinterpret_cast<uint4*>(lo + o) = lv;
         }
         if (lane == 0) scale[r] = __builtin_ldexpf(1.0f, e);
     }
@@ -738,19 +766,23 @@ void k_combine_pairs(const float* __restrict__ y, const float* __restrict__ w, u
 // launchers
 // ---------------------------------------------------------------------------
 template <int CPL, int TB, int ES = 1>
-static hipError_t route_c(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, float* normed,
-                          uint32_t* ids, float* w, float* logits, uint32_t* counters, hipStream_t s)
+static hipError_t route_c(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, uint16_t* x_hi,
+                          uint16_t* x_lo, float* x_sc, uint32_t* ids, float* w, float* logits, uint32_t* counters,
+                          hipStream_t s)
 {
     const dim3 grid(((T + TB - 1) / TB) * ES), block(ROUTE_WAVES * WAVE);
     if (d.E <= 128)
-        launch_kernel(k_route<CPL, TB, 2, ES>, grid, block, s, d, L, hidden, T, normed, ids, w, logits, counters);
+        launch_kernel(k_route<CPL, TB, 2, ES>, grid, block, s, d, L, hidden, T, x_hi, x_lo, x_sc, ids, w,
+                      logits, counters);
     else
-        launch_kernel(k_route<CPL, TB, 8, ES>, grid, block, s, d, L, hidden, T, normed, ids, w, logits, counters);
+        launch_kernel(k_route<CPL, TB, 8, ES>, grid, block, s, d, L, hidden, T, x_hi, x_lo, x_sc, ids, w,
+                      logits, counters);
     return hipGetLastError();
 }
 
-hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, float* normed,
-                        uint32_t* ids, float* w, float* logits, uint32_t* counters, hipStream_t s)
+hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidden, uint32_t T, uint16_t* x_hi,
+                        uint16_t* x_lo, float* x_sc, uint32_t* ids, float* w, float* logits, uint32_t* counters,
+                        hipStream_t s)
 {
     if (d.E > SMOE_TOPK_MAX_N || d.K > SMOE_TOPK_MAX_K || d.D % 64 || T == 0) return hipErrorInvalidValue;
     const uint32_t cpl = (d.D / 32 + WAVE - 1) / WAVE;
@@ -762,17 +794,17 @@ hipError_t launch_route(const MoeDims& d, const LayerDesc& L, const float* hidde
     const uint32_t tb = T >= 4 * cus ? 4 : T >= 2 * cus ? 2 : 1;
     const bool split = T < 128 && d.E <= 128 && logits && counters;
     if (cpl == 1) {
-        if (tb == 4) return route_c<1, 4>(d, L, hidden, T, normed, ids, w, logits, counters, s);
-        if (tb == 2) return route_c<1, 2>(d, L, hidden, T, normed, ids, w, logits, counters, s);
-        if (split) return route_c<1, 1, 4>(d, L, hidden, T, normed, ids, w, logits, counters, s);
-        return route_c<1, 1>(d, L, hidden, T, normed, ids, w, logits, counters, s);
+        if (tb == 4) return route_c<1, 4>(d, L, hidden, T, x_hi, x_lo, x_sc, ids, w, logits, counters, s);
+        if (tb == 2) return route_c<1, 2>(d, L, hidden, T, x_hi, x_lo, x_sc, ids, w, logits, counters, s);
+        if (split) return route_c<1, 1, 4>(d, L, hidden, T, x_hi, x_lo, x_sc, ids, w, logits, counters, s);
+        return route_c<1, 1>(d, L, hidden, T, x_hi, x_lo, x_sc, ids, w, logits, counters, s);
     }
     if (cpl == 2) {
-        if (tb >= 2) return route_c<2, 2>(d, L, hidden, T, normed, ids, w, logits, counters, s);
-        if (split) return route_c<2, 1, 4>(d, L, hidden, T, normed, ids, w, logits, counters, s);
-        return route_c<2, 1>(d, L, hidden, T, normed, ids, w, logits, counters, s);
+        if (tb >= 2) return route_c<2, 2>(d, L, hidden, T, x_hi, x_lo, x_sc, ids, w, logits, counters, s);
+        if (split) return route_c<2, 1, 4>(d, L, hidden, T, x_hi, x_lo, x_sc, ids, w, logits, counters, s);
+        return route_c<2, 1>(d, L, hidden, T, x_hi, x_lo, x_sc, ids, w, logits, counters, s);
     }
-    if (cpl <= 4) return route_c<4, 1>(d, L, hidden, T, normed, ids, w, logits, counters, s);
+    if (cpl <= 4) return route_c<4, 1>(d, L, hidden, T, x_hi, x_lo, x_sc, ids, w, logits, counters, s);
     return hipErrorInvalidValue;
 }
 
