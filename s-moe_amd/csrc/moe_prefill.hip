@@ -239,7 +239,7 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
         }
         uint32_t my_id;
         float my_w;
-        const uint32_t count = topk_fast<VPL>(p, d.E, d.K, d.norm_topk, my_id, my_w, s_slots[wv]);
+        const uint32_t count = topk_latency<VPL>(p, d.E, d.K, d.norm_topk, my_id, my_w, s_slots[wv]);
         if (static_cast<uint32_t>(lane) < count) {
             ids[static_cast<size_t>(t0 + wv) * d.K + lane] = my_id;
             w[static_cast<size_t>(t0 + wv) * d.K + lane] = my_w;
