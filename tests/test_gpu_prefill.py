@@ -177,3 +177,27 @@ def test_prefill_matches_decode(ctx):
     slack = np.spacing(np.abs(a.cpu().numpy())) + np.spacing(np.abs(b.cpu().numpy()))
     worst = max(rel_err(da[t], db[t], slack=slack[t])[0] for t in range(T))
     assert worst <= 2 * TOL   # both sides differ from the exact result by up to TOL
+
+
+def test_route_counters_across_launches(ctx, oracle):
+    """Short batches (under 128 tokens) split each token's router rows over 4
+    blocks that count themselves on per-token counters kept across launches
+    (never reset).  Consecutive calls with changing batch sizes, including
+    one of 300 tokens (one block per token, no counters) in between, must keep
+    every token's ids exact."""
+    layer = Layer(ctx, 2048, 128, 8, 768, layer_id=12)
+    for i, T in enumerate((40, 7, 127, 300, 1, 40, 64)):
+        h = hidden_states(ctx, T, layer.D, index0=50 + 17 * i)
+        h0 = h.cpu().numpy()
+        ids = torch.zeros((T, layer.K), dtype=torch.int32, device="cuda")
+        w = torch.zeros((T, layer.K), dtype=torch.float32, device="cuda")
+        ctx.moe_prefill(layer.shape, layer.layer, h.data_ptr(), T, ids.data_ptr(), w.data_ptr())
+        ctx.synchronize()
+        gids = ids.cpu().numpy().view(np.uint32)
+        gw = w.cpu().numpy()
+        for t in range(T):
+            x = oracle.rms_norm_bf16(h0[t], layer.h_norm)
+            logits = oracle.matvec_bf16(layer.h_router.reshape(layer.E, layer.D), x)
+            rid, rw = oracle.top_k(logits, layer.K, True)
+            assert (gids[t] == rid).all(), (T, t)
+            assert np.allclose(gw[t], rw, rtol=1e-5, atol=1e-7), (T, t)
