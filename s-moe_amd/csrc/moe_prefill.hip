@@ -91,6 +91,9 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
     // router rows per reduction batch (RPB * TB values); with ES > 1 a wave
     // has at most 4 rows (E <= 128 at ES = 4)
     constexpr int RPB = ES > 1 ? 4 : 16 / TB;
+    // the counters advance by ES per launch and token group, and one array
+    // serves every launch: a single split factor keeps their residues aligned
+    static_assert(ES == 1 || ES == 4, "one split factor for the route counters");
     __shared__ float s_logit[TB][SMOE_TOPK_MAX_N];
     __shared__ uint2 s_slots[TB][TOPK_SLOTS];
     __shared__ uint32_t s_last;
