@@ -193,8 +193,9 @@ __device__ uint32_t topk_fast(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t 
 // the top 8 keys in order.  The bit order is 5, 4 (v_permlane32/16_swap,
 // while the lists hold 2 and 4 keys and are merged whole by odd-even merges,
 // which compare equal indices only, so the swap's lane order does not
-// matter), then 3, 2, 1, 0 within rows (row_ror:8, row_half_mirror -- which
-// pairs quads that hold disjoint sets at that point -- and quad_perm), each
+// matter), then within rows: row_ror:8 (lane bit 3), row_half_mirror (lane
+// i with lane 7 - i of its 8: after bits 5, 4, 3 they hold the keys of lanes
+// with low bits i and 7 - i, disjoint sets) and quad_perm xor 2, xor 1, each
 // a bitonic top-8 merge.  The softmax (scout.cpp:85-98) runs beside the
 // network; it depends on the scores only.
 //
