@@ -16,14 +16,15 @@
 //                  columns of every 8 in the order 0 2 4 6 1 3 5 7.
 //   k_permute      stable counting sort of the T*k (token, rank) pairs by
 //                  expert (one workgroup), union order by first appearance.
-//   k_grouped_mm   per expert: [tokens x K] x [K x 64 rows] tiles on MFMA
-//                  v_mfma_f32_16x16x32_f16, activation chunks staged in LDS.
-//                  Weights enter exactly as (2c - 15)/8 (f16), activations as
-//                  hi and lo planes (two MFMAs into one fp32 accumulator);
-//                  each 64-column group adds s_g * sum, the row scale
-//                  8 * 2^e / 15 closes the dot (kernels.metal:90-105, 140-145).  Gate+up
-//                  runs with SiLU and writes h per (token, rank) pair; down
-//                  writes y per pair.
+//   k_grouped_mm   per expert: [pairs x K] x [K x rows] tiles (128 gate +
+//                  128 up rows, or 256 down rows, per block) on MFMA
+//                  v_mfma_f32_16x16x32_f16, weights and activation rows
+//                  streamed through LDS rings.  Weights enter exactly as
+//                  (2c - 15)/8 (f16), activations as hi and lo planes (two
+//                  MFMAs into one fp32 accumulator); each 64-column group adds
+//                  s_g * sum, the row scale 8 * 2^e / 15 closes the dot
+//                  (kernels.metal:90-105, 140-145).  Gate+up runs with SiLU
+//                  and writes h per (token, rank) pair; down writes y per pair.
 //   k_combine_pairs hidden[t] += sum_r w[t][r] * y[t*k + r] in rank order.
 //
 // Blocks of one expert are mapped to one XCD (block id mod 8), so its token
@@ -73,12 +74,14 @@ __device__ __forceinline__ void split8_f16(const float* x, int e, uint4& hi, uin
 // softmax/top-k (scout.cpp:77-123) for TB tokens per block of ROUTE_WAVES
 // waves.  Every wave normalises all TB tokens (lane l owns the 32-column
 // chunks l + 64 j) and computes router rows w, w + ROUTE_WAVES, ... for all of
-// them; wave t then selects the experts of token t.  With ES > 1 (short
-// batches) the E router rows of a token group are split over ES blocks, so
-// each wave has few rows and all their loads in flight at once: the blocks
-// write their logits to memory, count themselves on a device-scope counter
-// per token group, and the last one (count = ES - 1 modulo ES) runs the
-// group's top-k.
+// them; wave t then selects the experts of token t, and (in the group's
+// first block) writes token t's normed row as the GEMM's f16 planes.  With
+// ES > 1 (short batches) the E router rows of a token group are split over
+// ES blocks, so each wave has few rows and all their loads in flight at once:
+// the blocks write their logits with agent-scope stores, wait for them, and
+// add themselves to a device-scope counter per token group; the block that
+// finds the count at ES - 1 modulo ES runs the group's top-k on agent-scope
+// loads of the logits (no device-wide fence anywhere).
 // ---------------------------------------------------------------------------
 constexpr int ROUTE_WAVES = 8;
 
