@@ -149,6 +149,23 @@ def test_prefill_235b_shape(ctx, oracle):
     assert check_against_oracle(oracle, layer, h0, got, gids, gw) <= TOL
 
 
+def test_prefill_235b_512_tokens(ctx, oracle):
+    """512 tokens through one 235B-shaped layer (D=4096, I=1536): about 32
+    pairs per expert, so the grouped GEMM runs its 32- and 48-pair pass widths
+    over 64 groups.  Every token's ids exact; the hidden update on 8 tokens."""
+    layer = Layer(ctx, 4096, 128, 8, 1536, layer_id=13)
+    T = 512
+    h0, got, gids, gw, _ = run_prefill(ctx, layer, T, index0=2000)
+    for t in range(T):
+        x = oracle.rms_norm_bf16(h0[t], layer.h_norm)
+        logits = oracle.matvec_bf16(layer.h_router.reshape(layer.E, layer.D), x)
+        rid, rw = oracle.top_k(logits, layer.K, True)
+        assert (gids[t] == rid).all(), t
+        assert np.allclose(gw[t], rw, rtol=1e-5, atol=1e-7)
+    rows = np.linspace(0, T - 1, 8).astype(int)
+    assert check_against_oracle(oracle, layer, h0, got, gids, gw, rows=rows) <= TOL
+
+
 def test_prefill_multi_pass_and_no_renorm(ctx, oracle):
     """More tokens than one permute pass holds (E=512 lowers the limit), and
     norm_topk off."""
