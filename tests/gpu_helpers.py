@@ -71,3 +71,34 @@ def hidden_states(ctx, T, D, index0=0, seed=SEED):
     for t in range(T):
         ctx.synth_normal(h[t].data_ptr(), D, seed, smoe_amd.hidden_stream(index0 + t), 1.0)
     return h
+
+
+def q4_matrix_f64(layer, e, k):
+    """Matrix k (0 gate [I x D], 1 up [I x D], 2 down [D x I]) of expert e,
+    dequantised in fp64: (c - 7.5) / 7.5 * scale per 64-group, low nibble
+    first (shatter_moe.py:371-387)."""
+    blob = layer.h_pool[e * layer.stride:(e + 1) * layer.stride]
+    n = layer.D * layer.I
+    pk = blob[layer.off[2 * k]:layer.off[2 * k] + n // 2]
+    sc = blob[layer.off[2 * k + 1]:layer.off[2 * k + 1] + 2 * (n // 64)].view(np.float16).astype(np.float64)
+    codes = np.empty(n, np.float64)
+    codes[0::2] = pk & 15
+    codes[1::2] = pk >> 4
+    w = (codes - 7.5) / 7.5 * np.repeat(sc, 64)
+    return w.reshape((layer.I, layer.D) if k < 2 else (layer.D, layer.I))
+
+
+def moe_block_f64(layer, x, ids, w, mats=None):
+    """The MoE delta of one token in fp64 for given ids and weights: RMSNorm
+    (norm weights 1), then sum_r w_r * down(silu(gate x) * (up x))."""
+    mats = {} if mats is None else mats
+    x = np.asarray(x, np.float64)
+    xn = x / np.sqrt(np.mean(x * x) + 1e-6)
+    y = np.zeros(layer.D)
+    for r in range(len(ids)):
+        e = int(ids[r])
+        if e not in mats:
+            mats[e] = [q4_matrix_f64(layer, e, k) for k in range(3)]
+        g, u = mats[e][0] @ xn, mats[e][1] @ xn
+        y += float(w[r]) * (mats[e][2] @ (g / (1.0 + np.exp(-g)) * u))
+    return y

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import smoe_amd
-from gpu_helpers import Layer, hidden_states, moe_delta_err, rel_err
+from gpu_helpers import Layer, hidden_states, moe_block_f64, moe_delta_err, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -63,6 +63,28 @@ def test_layer_vs_oracle(ctx, oracle, D, E, K, I):
         e2, _ = rel_err(got, out)
         print(f"{D}x{E}x{K}x{I} rel_err delta={e1:.2e} hidden={e2:.2e}")
         assert max(e1, e2) <= TOL
+
+
+@pytest.mark.parametrize("D,E,K,I", [(2048, 128, 8, 768), (4096, 128, 8, 1536)])
+def test_layer_against_fp64(ctx, D, E, K, I):
+    """The one-launch decode layer against an fp64 evaluation of the block
+    (same ids and weights), at both Qwen3 shapes: the digit dot products and
+    exact integer sums keep the kernel well inside the oracle's own fp32
+    distance from fp64."""
+    layer = Layer(ctx, D, E, K, I, layer_id=D + I + 3)
+    mats = {}
+    worst = 0.0
+    for index0 in (5, 6, 7):
+        hid = hidden_states(ctx, 1, D, index0)[0]
+        h0 = hid.cpu().numpy()
+        gids, gw = decode(ctx, layer, hid)
+        got = hid.cpu().numpy().astype(np.float64)
+        y = moe_block_f64(layer, h0, gids, gw, mats)
+        slack = np.spacing(np.abs(got))          # the fp32 residual add
+        e, _ = rel_err(got - h0, y, slack=slack)
+        worst = max(worst, e)
+    print(f"{D}x{E}x{K}x{I} decode vs fp64: {worst:.2e}")
+    assert worst <= 5e-4
 
 
 @pytest.mark.parametrize("D,E,K,I", [SHAPES[0], SHAPES[1]])

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import Layer, hidden_states, rel_err
+from gpu_helpers import Layer, hidden_states, moe_block_f64, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -166,21 +166,6 @@ def test_prefill_235b_512_tokens(ctx, oracle):
     assert check_against_oracle(oracle, layer, h0, got, gids, gw, rows=rows) <= TOL
 
 
-def q4_matrix_f64(layer, e, k):
-    """Matrix k (0 gate [I x D], 1 up [I x D], 2 down [D x I]) of expert e,
-    dequantised in fp64: (c - 7.5) / 7.5 * scale per 64-group, low nibble
-    first (shatter_moe.py:371-387)."""
-    blob = layer.h_pool[e * layer.stride:(e + 1) * layer.stride]
-    n = layer.D * layer.I
-    pk = blob[layer.off[2 * k]:layer.off[2 * k] + n // 2]
-    sc = blob[layer.off[2 * k + 1]:layer.off[2 * k + 1] + 2 * (n // 64)].view(np.float16).astype(np.float64)
-    codes = np.empty(n, np.float64)
-    codes[0::2] = pk & 15
-    codes[1::2] = pk >> 4
-    w = (codes - 7.5) / 7.5 * np.repeat(sc, 64)
-    return w.reshape((layer.I, layer.D) if k < 2 else (layer.D, layer.I))
-
-
 def test_prefill_235b_against_fp64(ctx):
     """The grouped path against an fp64 evaluation of the same layer (same
     ids and weights), tighter than the oracle bound: the fp32 oracle itself
@@ -192,15 +177,7 @@ def test_prefill_235b_against_fp64(ctx):
     mats = {}
     worst = 0.0
     for t in range(T):
-        x = h0[t].astype(np.float64)
-        xn = x / np.sqrt(np.mean(x * x) + 1e-6)          # norm weights are 1
-        y = np.zeros(layer.D)
-        for r in range(layer.K):
-            e = int(gids[t, r])
-            if e not in mats:
-                mats[e] = [q4_matrix_f64(layer, e, k) for k in range(3)]
-            g, u = mats[e][0] @ xn, mats[e][1] @ xn
-            y += float(gw[t, r]) * (mats[e][2] @ (g / (1.0 + np.exp(-g)) * u))
+        y = moe_block_f64(layer, h0[t], gids[t], gw[t], mats)
         d_got = got[t].astype(np.float64) - h0[t]
         slack = np.spacing(np.abs(got[t])).astype(np.float64)   # the fp32 residual add
         e_t, _ = rel_err(d_got, y, slack=slack)
