@@ -227,7 +227,9 @@ def main():
         "metric": "MoE decode tok/s & achieved HBM GB/s, Qwen3-30B/235B-shaped Q4 layers",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 (Q4 weights; activations as 22-bit fixed point per 32-column chunk, exact int32 dot "
+                 "products; fp32 router, softmax, SiLU and combine)",
         "data": "synthetic (counter-based N(0,0.02) weights quantized to SMOE-Q4; N(0,1) hidden)",
         "config": {"workload": c["workload"], "d_model": D, "n_experts": E, "top_k": K, "d_ff": I,
                    "layers": NL, "batch": 1, "decode_steps": args.steps,
@@ -253,6 +255,10 @@ def main():
             "kernel": KERNEL_SYMBOLS[dom], "bytes_per_launch": kb[dom], "avg_us": kern[dom]["avg_us"],
             "timing": how,
         }
+        ceil = stream_ceiling(ctx, torch, pool)
+        if ceil:
+            line["roofline"]["ceiling"] = ceil
+            line["roofline"]["frac_of_ceiling"] = round(kern[dom]["gbs"] / ceil["achieved"], 4)
         line["kernels"] = kern
         layer_bytes = kb["decode_stack"] // NL
         line["layer_bytes"] = layer_bytes
@@ -281,6 +287,35 @@ def kernel_times(ctx, torch, stream, step, replays):
     return out, "hipExtLaunchKernel start/stop events on the launch stream, eager replays of the step"
 
 
+def stream_ceiling(ctx, torch, pool, launches=6):
+    """The device's streaming-read ceiling, measured in this run: k_stream_read
+    over the first 2 GiB of the expert pool (8x the Infinity Cache), timed by
+    its dispatch events like the decode kernels; the first launch is a
+    warm-up."""
+    import smoe_amd
+    nbytes = min(pool.numel(), 2 << 30) // 4096 * 4096
+    if nbytes < (256 << 20):
+        return None
+    sink = torch.zeros(1, dtype=torch.int32, device=pool.device)
+    ctx.stream_read(pool.data_ptr(), nbytes, sink.data_ptr())
+    torch.cuda.synchronize()
+    ctx.profile_enable(True)
+    for _ in range(launches):
+        ctx.stream_read(pool.data_ptr(), nbytes, sink.data_ptr())
+    torch.cuda.synchronize()
+    n, ms = ctx.profile_read(smoe_amd.KERNEL_STREAM)
+    ctx.profile_enable(False)
+    if not n:
+        return None
+    us = ms * 1e3 / n
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"streaming-read ceiling: {nbytes / 2**30:.1f} GiB in {us:.1f} us = {gbs:.0f} GB/s")
+    return {"achieved": round(gbs, 1), "unit": "GB/s", "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "kernel": "k_stream_read", "bytes": nbytes, "avg_us": round(us, 2),
+            "how": "non-temporal 128-bit loads, 1 KiB per wave instruction, 8 in flight per wave, "
+                   "2048 blocks x 4 waves, over the expert pool; dispatch events"}
+
+
 def _read_profile(ctx, smoe_amd):
     out = {}
     for kid, name in ((smoe_amd.KERNEL_MOE_UP, "moe_up"), (smoe_amd.KERNEL_MOE_DOWN, "moe_down"),
@@ -291,12 +326,31 @@ def _read_profile(ctx, smoe_amd):
     return out
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo, as lscpu reports it)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, target_s, engine="stack"):
-    """The CPU oracle (fp32 restatement, one thread) on whole decode steps of
-    the same stack, repeated until about `target_s` seconds of CPU work (at
-    least one step, at most 3 x target); host copies of the weights are made
-    before the timed region.  Also reports how far the GPU is from it on the
-    first step (layers teacher-forced on the oracle's own hidden state)."""
+    """The CPU oracle (fp32 restatement of the reference's arithmetic) on whole
+    decode steps of the same stack, timed two ways on this host: one thread
+    (the reference's CPU routing code is single-threaded) and every usable
+    core (OpenMP over output rows; each row keeps its sequential fp32 sum, so
+    the results are bit-identical, which is asserted).  Each leg: one warm-up
+    iteration, then the median of >= 5 timed iterations of whole steps, the
+    iteration size chosen so a leg takes about `target_s` / 2 seconds.  Host
+    copies of the weights are made before any timing.  For stacks too large
+    for a quick host copy (the 94-layer 235B stack) a stated prefix of layers
+    is timed and the per-layer time scaled to the whole stack.  Also reports
+    how far the GPU is from the oracle on the first step (layers
+    teacher-forced on the oracle's own hidden state)."""
     import numpy as np
     import torch
 
@@ -309,49 +363,80 @@ def cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, targ
     oshape = dict(d_model=D, n_experts=E, top_k=K, d_ff=I, group_size=64, norm_topk=1)
     h_norm = norm_w.cpu().numpy().view(np.uint16)
     layer_bytes = E * stride
-    log(f"cpu baseline: copying {NL} layers to host")
-    h_pools = [pool[l * layer_bytes:(l + 1) * layer_bytes].cpu().numpy() for l in range(NL)]
-    h_routers = [router[l].cpu().numpy().view(np.uint16) for l in range(NL)]
+    n_cpu = NL if NL * layer_bytes <= 20e9 else 8          # layers copied to the host
+    log(f"cpu baseline: copying {n_cpu} of {NL} layers to host")
+    h_pools = [pool[l * layer_bytes:(l + 1) * layer_bytes].cpu().numpy() for l in range(n_cpu)]
+    h_routers = [router[l].cpu().numpy().view(np.uint16) for l in range(n_cpu)]
+    cores = O.usable_cores()
 
-    # parity of the GPU against the oracle on step 0, layer by layer
+    def run_layers(h):
+        for l in range(n_cpu):
+            h = O.moe_decode_layer(oshape, h_norm, h_routers[l], h_pools[l], stride, off, h)[0]
+        return h
+
+    # parity of the GPU against the oracle on step 0, layer by layer (all cores)
     h = hidden0.cpu().numpy().astype(np.float32)
     gpu_h = hidden0.clone()
     ids = torch.zeros(K, dtype=torch.int32, device="cuda")
     id_mismatch, worst = 0, 0.0
-    total, steps = 0.0, 0
-    while True:
-        for l in range(NL):
-            if steps == 0:
-                gpu_h.copy_(torch.from_numpy(h))
-                lay = smoe_amd.make_layer(norm_w.data_ptr(), router[l].data_ptr(),
-                                          pool.data_ptr() + l * layer_bytes, stride, off)
-                if engine == "persistent":
-                    ctx.moe_decode_stack(shape, [lay], gpu_h.data_ptr(), ids.data_ptr())
-                else:
-                    ctx.moe_decode(shape, lay, gpu_h.data_ptr(), 1, ids.data_ptr())
-                torch.cuda.synchronize()
-            t0 = time.perf_counter()
+    with O.threads(cores):
+        for l in range(n_cpu):
+            gpu_h.copy_(torch.from_numpy(h))
+            lay = smoe_amd.make_layer(norm_w.data_ptr(), router[l].data_ptr(),
+                                      pool.data_ptr() + l * layer_bytes, stride, off)
+            if engine == "persistent":
+                ctx.moe_decode_stack(shape, [lay], gpu_h.data_ptr(), ids.data_ptr())
+            else:
+                ctx.moe_decode(shape, lay, gpu_h.data_ptr(), 1, ids.data_ptr())
+            torch.cuda.synchronize()
             out, oid, ow, _lg, _nr, yo = O.moe_decode_layer(oshape, h_norm, h_routers[l], h_pools[l], stride,
                                                             off, h)
-            total += time.perf_counter() - t0
-            if steps == 0:
-                g = gpu_h.cpu().numpy()
-                id_mismatch += int((ids.cpu().numpy().view(np.uint32) != oid).sum())
-                dref = (ow.astype(np.float64)[:, None] * yo.astype(np.float64)).sum(0)
-                tau = 1e-2 * np.sqrt(np.mean(dref ** 2))
-                diff = np.maximum(np.abs((g.astype(np.float64) - h) - dref) - np.spacing(np.abs(g)), 0.0)
-                worst = max(worst, float(np.max(diff / np.maximum(np.abs(dref), tau))))
+            g = gpu_h.cpu().numpy()
+            id_mismatch += int((ids.cpu().numpy().view(np.uint32) != oid).sum())
+            dref = (ow.astype(np.float64)[:, None] * yo.astype(np.float64)).sum(0)
+            tau = 1e-2 * np.sqrt(np.mean(dref ** 2))
+            diff = np.maximum(np.abs((g.astype(np.float64) - h) - dref) - np.spacing(np.abs(g)), 0.0)
+            worst = max(worst, float(np.max(diff / np.maximum(np.abs(dref), tau))))
             h = out
-        steps += 1
-        log(f"cpu baseline: {steps} step(s), {total:.1f} s")
-        if total >= target_s or total * (steps + 1) / steps > 3 * target_s:
-            break
+    h_first = h
+
+    def leg(n_threads, budget_s):
+        """median seconds per pass over the n_cpu layers, and the passes
+        per timed iteration"""
+        with O.threads(n_threads):
+            t0 = time.perf_counter()
+            h_out = run_layers(hidden0.cpu().numpy().astype(np.float32))      # warm-up
+            one = time.perf_counter() - t0
+            per_iter = max(1, int(budget_s / 5 / max(one, 1e-6)))
+            times = []
+            while len(times) < 5 or (sum(times) < budget_s and len(times) < 15):
+                t0 = time.perf_counter()
+                for _ in range(per_iter):
+                    run_layers(hidden0.cpu().numpy().astype(np.float32))
+                times.append((time.perf_counter() - t0) / per_iter)
+            log(f"cpu baseline: {n_threads} thread(s): {len(times)} iterations of {per_iter} pass(es), "
+                f"median {np.median(times):.3f} s per pass over {n_cpu} layers")
+        return float(np.median(times)), per_iter, len(times), h_out
+
+    t1, it1, n1, h1 = leg(1, target_s / 2)
+    tn, itn, nn, hn = leg(cores, target_s / 2)
+    if not (np.array_equal(h1, hn) and np.array_equal(h1, h_first)):
+        raise SystemExit("bench.py: the threaded CPU oracle differs from the single-threaded one")
+    scale = NL / n_cpu
+    tok1, tokn = 1.0 / (t1 * scale), 1.0 / (tn * scale)
+    expert_gb = (K * 3 * (D * I // 2 + D * I // 64 * 2) + 2 * E * D + 12 * D) * NL / 1e9
+    subset = "" if n_cpu == NL else f" (first {n_cpu} of {NL} layers timed, scaled to {NL})"
     return {
-        "value": round(steps / total, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-        "sample": f"{steps} decode step(s) through all {NL} layers (batch 1), oracle on one thread, "
-                  f"{total:.1f} s of CPU work; weights copied to host before timing",
-        "cpu_seconds": round(total, 3),
-        "parity_vs_gpu_step0": {"ids_mismatch": id_mismatch, "max_rel_err_moe_delta": float(f"{worst:.3e}")},
+        "value": round(tokn, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+        "sample": f"whole decode steps through the {NL}-layer stack (batch 1){subset}: oracle with OpenMP over "
+                  f"output rows on {cores} threads, median of {nn} iterations of {itn} step(s) after a warm-up; "
+                  f"weights copied to host before timing",
+        "gbs": round(expert_gb * tokn, 3),
+        "single_thread": {"value": round(tok1, 4), "unit": "tok/s", "cores": 1, "gbs": round(expert_gb * tok1, 3),
+                          "sample": f"median of {n1} iterations of {it1} step(s){subset}"},
+        "cpu_model": cpu_model(), "nproc": os.cpu_count(), "threads_bit_identical": True,
+        "parity_vs_gpu_step0": {"ids_mismatch": id_mismatch, "max_rel_err_moe_delta": float(f"{worst:.3e}"),
+                                "layers": n_cpu},
     }
 
 
@@ -364,19 +449,6 @@ GROUPED = {
     "batched": dict(D=4096, E=128, K=8, I=1536, T=64, zipf=1.1,
                     workload="qwen3-235b-a22b-moe-batched-decode-64-zipf1.1"),
 }
-
-
-def zipf_router(torch, ctx, smoe_amd, router, u, D, E, layer, s_exp):
-    """Router rows N(0, 0.02) plus b_e * u with b_e = -s ln(rank_e + 1) / 8
-    (rank = a seeded permutation of the experts), so that hidden states with
-    a fixed component along the unit vector u route with Zipf-like popularity
-    (the reference router has no bias term: this is a generator choice)."""
-    g = torch.Generator().manual_seed(SEED + layer)
-    rank = torch.randperm(E, generator=g).double()
-    b = -s_exp * torch.log(rank + 1.0) / 8.0
-    w = router.view(torch.bfloat16).float().view(E, D).double().cpu()
-    w = w + b[:, None] * u.double().cpu()[None, :]
-    router.copy_(w.float().to(torch.bfloat16).view(torch.int16).view(-1).cuda())
 
 
 def trunk_bench(args):
@@ -634,13 +706,13 @@ def grouped_bench(args):
         ctx.synth_normal(h0[t].data_ptr(), D, SEED, smoe_amd.hidden_stream(t), 1.0)
     u = None
     if g["zipf"]:
-        u = torch.randn(D, generator=torch.Generator().manual_seed(SEED), dtype=torch.float64)
-        u = (u / u.norm()).float().cuda()
-        h0 += 8.0 * u[None, :]          # a fixed component along u (|x . u| ~ 8 of ~64 norm)
+        from smoe_amd import synthetic
+        u = synthetic.zipf_direction(D, SEED)
+        synthetic.zipf_hidden(h0, u)     # a fixed component along u (|x . u| = 8 of ~64 norm)
     for l in range(R):
         ctx.synth_bf16(router[l].data_ptr(), E * D, SEED, smoe_amd.router_stream(l), 0.02)
         if u is not None:
-            zipf_router(torch, ctx, smoe_amd, router[l], u, D, E, l, g["zipf"])
+            synthetic.zipf_bias_router(router[l], u, D, E, l, g["zipf"], SEED)
     layers = [smoe_amd.make_layer(norm_w.data_ptr(), router[l].data_ptr(), pool.data_ptr() + l * E * stride,
                                   stride, off) for l in range(R)]
     hidden = h0.clone()

@@ -424,9 +424,18 @@ const char* smoe_hip_vault_error(void);
 #define SMOE_KERNEL_MOE_LAYER    12   /* decode: the whole MoE block of one token in one launch */
 #define SMOE_KERNEL_GEMV         13   /* dense trunk: grouped bf16 GEMV                          */
 #define SMOE_KERNEL_ATTENTION    14   /* dense trunk: QK norm/RoPE/KV append + decode attention   */
+#define SMOE_KERNEL_STREAM       15   /* measurement: streaming-read ceiling (smoe_hip_stream_read) */
 #define SMOE_KERNEL_KINDS        16
 int smoe_hip_profile_enable(SmoeMetalCtx* ctx, int enable);
 int smoe_hip_profile_read(SmoeMetalCtx* ctx, uint32_t kernel, uint64_t* launches, double* total_ms);
+
+/* Measurement only (no counterpart in the reference): reads `bytes` (a
+ * multiple of 16) of device memory at `src` with non-temporal 128-bit loads
+ * in one launch on the context's stream and XORs a fold of them into the
+ * device word *sink.  Timed like the other kernels, it gives the streaming
+ * ceiling that decode rooflines are quoted against beside the datasheet
+ * peak. */
+int smoe_hip_stream_read(SmoeMetalCtx* ctx, const void* src, uint64_t bytes, uint32_t* sink);
 
 /* last HIP error string seen by this context ("" if none) */
 const char* smoe_hip_last_error(const SmoeMetalCtx* ctx);

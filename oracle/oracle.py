@@ -106,6 +106,9 @@ def lib():
         L.orc_union_w.argtypes = [C.c_uint32, C.c_uint32]
         L.orc_moe_prefill_layer.argtypes = [C.POINTER(OrcShape), C.POINTER(OrcLayer), _f32p,
                                             C.c_uint32, _u32p, _f32p]
+        L.orc_set_threads.argtypes = [C.c_int]
+        L.orc_get_threads.restype = C.c_int
+        L.orc_max_threads.restype = C.c_int
         _lib = L
     return _lib
 
@@ -147,6 +150,33 @@ def ref():
 # --------------------------------------------------------------------------
 # numpy-level helpers
 # --------------------------------------------------------------------------
+
+def usable_cores() -> int:
+    """Host cores this process may use: the CPU affinity mask, capped by
+    OMP_NUM_THREADS when that is set."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+class threads:
+    """Context manager: the oracle's row-parallel loops on n threads (results
+    are bit-identical for any n)."""
+
+    def __init__(self, n: int):
+        self.n = max(1, int(n))
+
+    def __enter__(self):
+        self.prev = lib().orc_get_threads()
+        lib().orc_set_threads(self.n)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_threads(self.prev)
+        return False
+
 
 def gen_normal(n, seed, stream, stddev=1.0):
     out = np.empty(n, np.float32)

@@ -12,6 +12,26 @@
 #include <stdlib.h>
 #include <string.h>
 
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* Threads of the row-parallel loops (orc_set_threads).  Every output row is
+ * one sequential fp32 sum computed by one thread, so results do not depend on
+ * the thread count. */
+static int g_threads = 1;
+
+void orc_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+int orc_get_threads(void) { return g_threads; }
+int orc_max_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
 static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 
@@ -226,6 +246,7 @@ void orc_rms_norm_bf16(float* x, const uint16_t* w, uint32_t n)   /* :245-256 */
 void orc_matvec_bf16(float* out, const uint16_t* weight, const float* in,
                      uint32_t rows, uint32_t cols)                 /* :293-306 */
 {
+#pragma omp parallel for num_threads(g_threads) schedule(static) if (g_threads > 1)
     for (uint32_t i = 0; i < rows; ++i) {
         float sum = 0.0f;
         const uint16_t* w_row = weight + (size_t)i * cols;
@@ -319,13 +340,32 @@ void orc_expert_ffn(const uint8_t* pg, const uint16_t* sg,
                     const float* x, float* hidden, float* out,
                     uint32_t d_ff, uint32_t d_model, uint32_t group)
 {
+#pragma omp parallel num_threads(g_threads) if (g_threads > 1)
+    {
+#pragma omp for schedule(static)
+        for (uint32_t r = 0; r < d_ff; ++r) {
+            float g = q4_row_dot(pg, sg, r, d_model, group, x);
+            float u = q4_row_dot(pu, su, r, d_model, group, x);
+            hidden[r] = orc_silu(g) * u;                   /* kernels.metal:720-722 */
+        }
+        /* (the implicit barrier of the loop above: down needs all of hidden) */
+#pragma omp for schedule(static)
+        for (uint32_t d = 0; d < d_model; ++d)
+            out[d] = q4_row_dot(pd, sd, d, d_ff, group, hidden);
+    }
+}
+
+/* The same FFN with one thread, for callers that already run in parallel. */
+static void expert_ffn_serial(const uint8_t* pg, const uint16_t* sg, const uint8_t* pu, const uint16_t* su,
+                              const uint8_t* pd, const uint16_t* sd, const float* x, float* hidden, float* out,
+                              uint32_t d_ff, uint32_t d_model, uint32_t group)
+{
     for (uint32_t r = 0; r < d_ff; ++r) {
         float g = q4_row_dot(pg, sg, r, d_model, group, x);
         float u = q4_row_dot(pu, su, r, d_model, group, x);
-        hidden[r] = orc_silu(g) * u;                       /* kernels.metal:720-722 */
+        hidden[r] = orc_silu(g) * u;
     }
-    for (uint32_t d = 0; d < d_model; ++d)
-        out[d] = q4_row_dot(pd, sd, d, d_ff, group, hidden);
+    for (uint32_t d = 0; d < d_model; ++d) out[d] = q4_row_dot(pd, sd, d, d_ff, group, hidden);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -465,8 +505,11 @@ void orc_moe_prefill_layer(const OrcShape* s, const OrcLayer* L, float* hidden,
     float* normed = (float*)malloc((size_t)ORC_CHUNK * D * sizeof(float));
     float* routed = (float*)malloc((size_t)ORC_CHUNK * D * sizeof(float));
     float* logits = (float*)malloc(E * sizeof(float));
-    float* h = (float*)malloc(I * sizeof(float));
-    float* y = (float*)malloc(D * sizeof(float));
+    const size_t max_pairs = (size_t)ORC_CHUNK * K;
+    float* py = (float*)malloc(max_pairs * D * sizeof(float));
+    uint32_t* pe = (uint32_t*)malloc(max_pairs * sizeof(uint32_t));
+    uint32_t* pt = (uint32_t*)malloc(max_pairs * sizeof(uint32_t));
+    float* pw = (float*)malloc(max_pairs * sizeof(float));
     uint32_t tid[32];
     float tw[32];
 
@@ -487,18 +530,36 @@ void orc_moe_prefill_layer(const OrcShape* s, const OrcLayer* L, float* hidden,
                 if (tid[e] < ORC_MAX_EXPERTS) orc_union_add(tid[e], i, tw[e]);
             }
         }
-        for (uint32_t u = 0; u < g_union_size; ++u) {            /* :339-417 */
-            uint32_t eid = g_union_ids[u];
-            const OrcExpertTokens* et = &g_elist[eid];
-            const uint8_t *pg, *pu, *pd; const uint16_t *sg, *su, *sd;
-            expert_ptrs(L, eid, &pg, &sg, &pu, &su, &pd, &sd);
+        /* :339-417: every (expert, token) pair of the chunk, listed in union
+         * order; the FFNs are independent (computed in parallel when threads
+         * are set), the scatter into routed_out keeps the reference's order */
+        uint32_t np_ = 0;
+        for (uint32_t u = 0; u < g_union_size; ++u) {
+            const OrcExpertTokens* et = &g_elist[g_union_ids[u]];
             for (uint32_t t = 0; t < et->count; ++t) {
-                orc_expert_ffn(pg, sg, pu, su, pd, sd, normed + (size_t)et->tok[t] * D,
-                               h, y, I, D, s->group_size);
-                float* ro = routed + (size_t)et->tok[t] * D;     /* :380-385 */
-                const float wt = et->w[t];
-                for (uint32_t d = 0; d < D; ++d) ro[d] += wt * y[d];
+                pe[np_] = g_union_ids[u];
+                pt[np_] = et->tok[t];
+                pw[np_] = et->w[t];
+                ++np_;
             }
+        }
+#pragma omp parallel num_threads(g_threads) if (g_threads > 1)
+        {
+            float* hh = (float*)malloc(I * sizeof(float));
+#pragma omp for schedule(dynamic, 1)
+            for (uint32_t p = 0; p < np_; ++p) {
+                const uint8_t *pg, *pu, *pd; const uint16_t *sg, *su, *sd;
+                expert_ptrs(L, pe[p], &pg, &sg, &pu, &su, &pd, &sd);
+                expert_ffn_serial(pg, sg, pu, su, pd, sd, normed + (size_t)pt[p] * D, hh,
+                                  py + (size_t)p * D, I, D, s->group_size);
+            }
+            free(hh);
+        }
+        for (uint32_t p = 0; p < np_; ++p) {                     /* :380-385 */
+            float* ro = routed + (size_t)pt[p] * D;
+            const float* y = py + (size_t)p * D;
+            const float wt = pw[p];
+            for (uint32_t d = 0; d < D; ++d) ro[d] += wt * y[d];
         }
         for (uint32_t i = 0; i < B; ++i) {                       /* :446-451 */
             float* hh = hidden + (size_t)(c0 + i) * D;
@@ -506,7 +567,7 @@ void orc_moe_prefill_layer(const OrcShape* s, const OrcLayer* L, float* hidden,
             for (uint32_t d = 0; d < D; ++d) hh[d] += ro[d];
         }
     }
-    free(normed); free(routed); free(logits); free(h); free(y);
+    free(normed); free(routed); free(logits); free(py); free(pe); free(pt); free(pw);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -39,6 +39,15 @@
 extern "C" {
 #endif
 
+/* ---- threads ---------------------------------------------------------------
+ * Row-parallel loops (OpenMP) in orc_matvec_bf16, orc_expert_ffn and the
+ * per-pair FFNs of orc_moe_prefill_layer.  Each output row remains one
+ * sequential fp32 sum on one thread, so every result is bit-identical for
+ * any thread count (1 = the reference's single-threaded loops). */
+void orc_set_threads(int n);
+int  orc_get_threads(void);
+int  orc_max_threads(void);
+
 /* ---- number formats ------------------------------------------------------ */
 float    orc_bf16_to_f32(uint16_t b);
 uint16_t orc_f32_to_bf16(float f);          /* round to nearest even */

@@ -751,6 +751,15 @@ extern "C" int smoe_hip_synchronize(SmoeMetalCtx* ctx)
     return SMOE_OK;
 }
 
+extern "C" int smoe_hip_stream_read(SmoeMetalCtx* ctx, const void* src, uint64_t bytes, uint32_t* sink)
+{
+    if (!ctx || !src || !sink || bytes < 16 || bytes % 16) return SMOE_ERR_ARG;
+    if (!timed(ctx, SMOE_KERNEL_STREAM, "stream_read",
+               [&] { return smoe::launch_stream_read(src, bytes, sink, ctx->stream); }))
+        return SMOE_ERR_HIP;
+    return SMOE_OK;
+}
+
 extern "C" int smoe_hip_set_decode_engine(SmoeMetalCtx* ctx, int engine)
 {
     if (!ctx || (engine != SMOE_DECODE_LAUNCHES && engine != SMOE_DECODE_PERSISTENT && engine != SMOE_DECODE_SPLIT))

@@ -206,6 +206,11 @@ hipError_t launch_grouped_down(const MoeDims& d, const LayerDesc& L, const uint3
 hipError_t launch_combine_pairs(const float* y, const float* w, uint32_t T, uint32_t K, uint32_t D, float* hidden,
                                 hipStream_t s);
 
+// ---- measurement (probe.hip) ----------------------------------------------
+// Streams `bytes` (a multiple of 16) from src with non-temporal 128-bit loads;
+// folds what it read into *sink.
+hipError_t launch_stream_read(const void* src, uint64_t bytes, uint32_t* sink, hipStream_t s);
+
 // ---- synthetic generator / quantizer (synth.hip) -------------------------
 hipError_t launch_synth_normal(float* out, uint64_t n, uint64_t seed, uint64_t stream,
                                float stddev, hipStream_t s);

@@ -159,15 +159,17 @@ struct StackLayout {
 
 size_t stack_xch_words(const MoeDims& d, uint32_t n_layers) { return StackLayout(d).layer * n_layers; }
 
-// CPL: 32-column chunks of D per lane (1: D <= 2048, 2: D <= 4096);
 // VPL/RRW: logits per lane / router rows per wave (2/1: E <= 128, 8/4: E <= 512);
 // CW: lanes per down row, a power of two >= I / 32 (8, 32 or 64).
-template <int CPL, int VPL, int RRW, int CW>
+// d_model <= 2048 only (stack_supported): one 32-column chunk of D per lane,
+// and at most 16 combine rows per wave (D / 128), which is what y_s holds.
+template <int VPL, int RRW, int CW>
 __global__ __launch_bounds__(ST_THREADS, 1)
 void k_decode_stack(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_layers, float* __restrict__ hidden,
                     uint64_t* __restrict__ xch, uint32_t* __restrict__ ctl, uint32_t* __restrict__ ids_out,
                     float* __restrict__ w_out, uint32_t* __restrict__ err)
 {
+    constexpr int CPL = 1;                       // 32-column chunks of D per lane
     constexpr int HG = 2 * CPL;                  // float4 groups of hidden per thread
     constexpr int HGI = (CW * 8 + ST_THREADS - 1) / ST_THREADS;   // float4 groups of h per thread
     constexpr int SEG = ilog2(CW);
@@ -421,7 +423,8 @@ void k_decode_stack(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_
             const bool cact = cI < nchI;
             const uint32_t cIc = min(cI, nchI - 1);
             for (uint32_t r = x; r < K; r += 8) {
-                const uint32_t e = readlane_u32(my_id, static_cast<int>(r));
+                // (clamped: ids from a timed-out exchange must still index inside the pool)
+                const uint32_t e = min(readlane_u32(my_id, static_cast<int>(r)), E - 1);
                 const uint8_t* blob = Ld.experts + size_t(e) * Ld.stride;
                 const uint8_t* pg = blob + Ld.off[0];
                 const uint16_t* sg = reinterpret_cast<const uint16_t*>(blob + Ld.off[1]);
@@ -565,7 +568,7 @@ void k_decode_stack(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_
             // block's rows of all ranks (a quarter of the cross-XCD requests
             // of every wave polling its own) and hands them over through LDS.
             {
-                const uint32_t rpc = (D + ST_WX - 1) / ST_WX;          // rows per wave (<= 16)
+                const uint32_t rpc = (D + ST_WX - 1) / ST_WX;          // rows per wave (<= 16: D <= 2048)
                 const uint32_t brow0 = (jw - wv) * rpc;                 // the block's first row
                 if (wv == 0) {
                     const uint32_t br = brow0 + lane;
@@ -638,30 +641,28 @@ void k_decode_stack(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_
 // ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
-// d_model up to 2048 (one 32-column chunk per lane).  The two-chunk variant
-// (d_model up to 4096) is switched off: it faulted once on MI355X (memory
-// aperture violation) and no cause has been found in its indexing; those
-// shapes run through the per-layer kernels.
+// d_model up to 2048 (one 32-column chunk per lane, D / 128 <= 16 combine
+// rows per wave); larger shapes run through the per-layer kernels.
 bool stack_supported(const MoeDims& d)
 {
     return d.group == 64 && d.D % 64 == 0 && d.D <= 2048 && d.I % 64 == 0 && d.I <= 2048 && d.E >= 1 &&
            d.E <= 512 && d.K >= 1 && d.K <= static_cast<uint32_t>(SMOE_TOPK_MAX_K) && d.K <= d.E;
 }
 
-template <int CPL, int VPL, int RRW>
+template <int VPL, int RRW>
 static void stack_cw(const MoeDims& d, const LayerDesc* layers, uint32_t n_layers, float* hidden, uint64_t* xch,
                      uint32_t* ctl, uint32_t* ids, float* w, uint32_t* err, hipStream_t s)
 {
     const uint32_t nchI = d.I / 32;
     const dim3 grid(ST_BLOCKS), block(ST_THREADS);
     if (nchI <= 8)
-        launch_kernel(k_decode_stack<CPL, VPL, RRW, 8>, grid, block, s, d, layers, n_layers, hidden, xch, ctl, ids, w,
+        launch_kernel(k_decode_stack<VPL, RRW, 8>, grid, block, s, d, layers, n_layers, hidden, xch, ctl, ids, w,
                       err);
     else if (nchI <= 32)
-        launch_kernel(k_decode_stack<CPL, VPL, RRW, 32>, grid, block, s, d, layers, n_layers, hidden, xch, ctl, ids,
+        launch_kernel(k_decode_stack<VPL, RRW, 32>, grid, block, s, d, layers, n_layers, hidden, xch, ctl, ids,
                       w, err);
     else
-        launch_kernel(k_decode_stack<CPL, VPL, RRW, 64>, grid, block, s, d, layers, n_layers, hidden, xch, ctl, ids,
+        launch_kernel(k_decode_stack<VPL, RRW, 64>, grid, block, s, d, layers, n_layers, hidden, xch, ctl, ids,
                       w, err);
 }
 
@@ -669,8 +670,8 @@ hipError_t launch_decode_stack(const MoeDims& d, const LayerDesc* layers, uint32
                                uint64_t* xch, uint32_t* ctl, uint32_t* ids, float* w, uint32_t* err, hipStream_t s)
 {
     if (!stack_supported(d) || n_layers == 0 || n_layers > ST_MAX_LAYERS) return hipErrorInvalidValue;
-    if (d.E <= 128) stack_cw<1, 2, 1>(d, layers, n_layers, hidden, xch, ctl, ids, w, err, s);
-    else stack_cw<1, 8, 4>(d, layers, n_layers, hidden, xch, ctl, ids, w, err, s);
+    if (d.E <= 128) stack_cw<2, 1>(d, layers, n_layers, hidden, xch, ctl, ids, w, err, s);
+    else stack_cw<8, 4>(d, layers, n_layers, hidden, xch, ctl, ids, w, err, s);
     return hipGetLastError();
 }
 

@@ -177,15 +177,17 @@ extern "C" int smoe_hip_vault_open(const char* path, SmoeVault** out)
     if (h.group_size != 64) return fail(SMOE_ERR_SHAPE, "vault: group size %u (SMOE-Q4 uses 64)", h.group_size);
     const uint64_t table_bytes = uint64_t(h.total_experts) * sizeof(VEntry);
     const uint64_t desc_bytes = uint64_t(h.total_experts) * 3 * sizeof(VDesc);
-    if (h.table_offset < sizeof(VHeader) || h.table_offset + table_bytes + desc_bytes > h.data_offset ||
-        h.data_offset > v->file_size)
+    // (every bound below is checked in subtraction form: sums of file-supplied
+    // 64-bit values could wrap)
+    if (h.table_offset < sizeof(VHeader) || h.data_offset > v->file_size || h.table_offset > h.data_offset ||
+        table_bytes + desc_bytes > h.data_offset - h.table_offset)
         return fail(SMOE_ERR_VAULT, "vault: expert table [%llu, +%llu) does not fit before data offset %llu",
                     (unsigned long long)h.table_offset, (unsigned long long)(table_bytes + desc_bytes),
                     (unsigned long long)h.data_offset);
 
     // v2 arch block (main.cpp:125-157): required, checked, never guessed
     if (h.version >= 2) {
-        if (h.reserved_ext == 0 || uint64_t(h.reserved_ext) + sizeof(VArch) > h.data_offset)
+        if (h.reserved_ext == 0 || h.data_offset < sizeof(VArch) || h.reserved_ext > h.data_offset - sizeof(VArch))
             return fail(SMOE_ERR_VAULT, "vault: v2 vault has no valid arch-block offset");
         if (!read_at(fd, &v->arch, sizeof(VArch), h.reserved_ext) ||
             std::memcmp(v->arch.magic, kArchMagic, 4) != 0 || v->arch.block_size != sizeof(VArch) ||
@@ -219,7 +221,7 @@ extern "C" int smoe_hip_vault_open(const char* path, SmoeVault** out)
         const VEntry& e = v->table[i];
         const VDesc* dd = &v->descs[size_t(i) * 3];
         if (e.byte_offset < h.data_offset || e.byte_offset % kPage != 0 || e.raw_size > e.padded_size ||
-            e.byte_offset + e.raw_size > v->file_size)
+            e.padded_size % kPage != 0 || e.byte_offset > v->file_size || e.raw_size > v->file_size - e.byte_offset)
             return fail(SMOE_ERR_VAULT, "vault: blob of layer %u expert %u at %llu (+%llu) is misplaced", e.layer_id,
                         e.expert_id, (unsigned long long)e.byte_offset, (unsigned long long)e.raw_size);
         if (e.raw_size != e0.raw_size || e.padded_size != e0.padded_size)
@@ -231,9 +233,14 @@ extern "C" int smoe_hip_vault_open(const char* path, SmoeVault** out)
             const uint64_t n = uint64_t(x.rows) * x.cols;
             if (x.tensor_type != t || x.ndim != 2 || x.rows != want_rows || x.cols != want_cols ||
                 x.packed_size != n / 2 || x.scales_size != n / h.group_size * 2 || n % h.group_size != 0 ||
-                x.packed_offset + x.packed_size > e.raw_size || x.scales_offset + x.scales_size > e.raw_size)
+                x.packed_offset > e.raw_size || x.packed_size > e.raw_size - x.packed_offset ||
+                x.scales_offset > e.raw_size || x.scales_size > e.raw_size - x.scales_offset)
                 return fail(SMOE_ERR_VAULT, "vault: descriptor %d of layer %u expert %u does not describe a %ux%u "
                             "SMOE-Q4 matrix inside its blob", t, e.layer_id, e.expert_id, want_rows, want_cols);
+            // the kernels read packed rows with 16-byte loads and scales as fp16
+            if (x.packed_offset % 16 != 0 || x.scales_offset % 2 != 0)
+                return fail(SMOE_ERR_VAULT, "vault: descriptor %d of layer %u expert %u: tensor offsets not aligned "
+                            "(packed %% 16, scales %% 2)", t, e.layer_id, e.expert_id);
             if (x.packed_offset != d0[t].packed_offset || x.scales_offset != d0[t].scales_offset)
                 return fail(SMOE_ERR_VAULT, "vault: layer %u expert %u lays its tensors out unlike expert 0",
                             e.layer_id, e.expert_id);

@@ -128,16 +128,18 @@ SIGNATURES = [
     ("smoe_hip_profile_enable", _I, [_VP, _I]),
     ("smoe_hip_profile_read", _I, [_VP, _U32, C.POINTER(C.c_uint64), C.POINTER(C.c_double)]),
     ("smoe_hip_last_error", C.c_char_p, [_VP]),
+    ("smoe_hip_stream_read", _I, [_VP, _VP, _U64, _VP]),
 ]
 
 KERNEL_MOE_UP, KERNEL_GATE_UP, KERNEL_MOE_DOWN, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
 KERNEL_PERMUTE, KERNEL_GROUPED_GATE_UP, KERNEL_GROUPED_DOWN, KERNEL_SCATTER = 5, 6, 7, 8
 KERNEL_ROUTE, KERNEL_SPLIT, KERNEL_STACK, KERNEL_MOE_LAYER = 9, 10, 11, 12
-KERNEL_GEMV, KERNEL_ATTENTION = 13, 14
+KERNEL_GEMV, KERNEL_ATTENTION, KERNEL_STREAM = 13, 14, 15
 DECODE_LAUNCHES, DECODE_PERSISTENT, DECODE_SPLIT = 0, 1, 2
 KERNEL_NAMES = {0: "moe_up", 1: "gate_up", 2: "moe_down", 3: "down_slots", 4: "topk",
                 5: "permute", 6: "grouped_gate_up", 7: "grouped_down", 8: "combine", 9: "route",
-                10: "split", 11: "decode_stack", 12: "moe_layer", 13: "gemv", 14: "attention"}
+                10: "split", 11: "decode_stack", 12: "moe_layer", 13: "gemv", 14: "attention",
+                15: "stream_read"}
 
 _lib = None
 
@@ -321,6 +323,10 @@ class Context:
         ms = C.c_double()
         self._check(self.lib.smoe_hip_profile_read(self.ptr, kernel, C.byref(n), C.byref(ms)), "profile_read")
         return int(n.value), float(ms.value)
+
+    def stream_read(self, src: int, nbytes: int, sink: int):
+        """Measurement: one streaming read of nbytes at src (the HBM ceiling)."""
+        self._check(self.lib.smoe_hip_stream_read(self.ptr, src, nbytes, sink), "stream_read")
 
     def dispatches(self) -> int:
         return int(self.lib.smoe_metal_kernel_dispatches(self.ptr))

@@ -53,9 +53,14 @@ class Layer:
                                          self.pool.data_ptr(), self.stride, self.off)
         torch.cuda.synchronize()
         if host:
-            self.h_pool = self.pool.cpu().numpy()
-            self.h_router = self.router.cpu().numpy().view(np.uint16)
-            self.h_norm = self.norm_w.cpu().numpy().view(np.uint16)
+            self.host_copies()
+
+    def host_copies(self):
+        """Copies of the device weights for the oracle (again after a change)."""
+        torch.cuda.synchronize()
+        self.h_pool = self.pool.cpu().numpy()
+        self.h_router = self.router.cpu().numpy().view(np.uint16)
+        self.h_norm = self.norm_w.cpu().numpy().view(np.uint16)
 
     def oracle_shape(self):
         return dict(d_model=self.D, n_experts=self.E, top_k=self.K, d_ff=self.I, group_size=64,
@@ -102,3 +107,22 @@ def moe_block_f64(layer, x, ids, w, mats=None):
         g, u = mats[e][0] @ xn, mats[e][1] @ xn
         y += float(w[r]) * (mats[e][2] @ (g / (1.0 + np.exp(-g)) * u))
     return y
+
+
+def moe_delta_f64_batch(layer, X, ids, w):
+    """The MoE delta of every row of X [T x D] in fp64 for given ids / weights
+    [T x K] (RMSNorm with norm weights 1, then sum_r w_r * down(silu(gate x) *
+    (up x)) in rank order), one expert's matrices dequantised at a time."""
+    X = np.asarray(X, np.float64)
+    Xn = X / np.sqrt(np.mean(X * X, axis=1, keepdims=True) + 1e-6)
+    T, K = ids.shape
+    Y = np.zeros((T, K, layer.D))
+    for e in np.unique(ids):
+        t, r = np.nonzero(ids == e)
+        G, U, Dn = (q4_matrix_f64(layer, int(e), k) for k in range(3))
+        g, u = Xn[t] @ G.T, Xn[t] @ U.T
+        Y[t, r] = (g / (1.0 + np.exp(-g)) * u) @ Dn.T
+    out = np.zeros((T, layer.D))
+    for r in range(K):
+        out += np.asarray(w, np.float64)[:, r:r + 1] * Y[:, r]
+    return out

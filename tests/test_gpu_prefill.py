@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import Layer, hidden_states, moe_block_f64, rel_err
+from gpu_helpers import Layer, hidden_states, moe_block_f64, moe_delta_f64_batch, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -65,8 +65,8 @@ def test_permute_rejects_bad_ids(ctx):
     ctx.synchronize()    # the flag is reported once, then cleared
 
 
-def run_prefill(ctx, layer, T, index0=0, perm=False):
-    h = hidden_states(ctx, T, layer.D, index0=index0)
+def run_prefill(ctx, layer, T, index0=0, perm=False, h=None):
+    h = hidden_states(ctx, T, layer.D, index0=index0) if h is None else h
     h0 = h.cpu().numpy()
     ids = torch.zeros((T, layer.K), dtype=torch.int32, device="cuda")
     w = torch.zeros((T, layer.K), dtype=torch.float32, device="cuda")
@@ -85,10 +85,28 @@ def run_prefill(ctx, layer, T, index0=0, perm=False):
     return h0, h.cpu().numpy(), ids.cpu().numpy().view(np.uint32), w.cpu().numpy(), extra
 
 
-def check_against_oracle(oracle, layer, h0, got, gids, gw, rows=None):
+F64_TOL = 5e-4
+
+
+def check_against_oracle(oracle, layer, h0, got, gids, gw, rows=None, exact=False):
+    """Worst relative error of the GPU's MoE delta against the oracle's over
+    `rows`, after asserting their ids / weights.
+
+    With exact=True every checked token is also evaluated in fp64 (same ids
+    and weights) and two things are asserted or returned:
+      * the GPU delta within F64_TOL of the fp64 delta (asserted);
+      * against the oracle, the excess of |gpu - oracle| over the oracle's
+        own distance from fp64 at that element (returned): at d_model 4096
+        the oracle's sequential fp32 sums over 4096 and 1536 terms -- the
+        reference's batch-kernel arithmetic, kernels.metal:672-769 -- round
+        to up to ~1e-3 of an element near the 1 % floor, more than the
+        kernels do, so the plain distance can exceed 1e-3 while the GPU is the
+        closer of the two to the exact value."""
     rows = np.arange(h0.shape[0]) if rows is None else rows
-    ref, rids, rw = oracle.moe_prefill_layer(layer.oracle_shape(), layer.h_norm, layer.h_router, layer.h_pool,
-                                             layer.stride, layer.off, h0[rows])
+    # (threaded oracle: bit-identical to its single-threaded loops)
+    with oracle.threads(oracle.usable_cores()):
+        ref, rids, rw = oracle.moe_prefill_layer(layer.oracle_shape(), layer.h_norm, layer.h_router,
+                                                 layer.h_pool, layer.stride, layer.off, h0[rows])
     assert (gids[rows] == rids).all(), np.argwhere(gids[rows] != rids)[:5]
     assert np.allclose(gw[rows], rw, rtol=1e-5, atol=1e-7)
     # MoE delta of every token; the residual add is rounded once on each side
@@ -100,7 +118,19 @@ def check_against_oracle(oracle, layer, h0, got, gids, gw, rows=None):
         e, _ = rel_err(d_got[i], d_ref[i], slack=slack[i])
         worst = max(worst, e)
     print(f"prefill rel_err (delta) {worst:.2e} over {len(rows)} tokens")
-    return worst
+    if not exact:
+        return worst
+    x64 = moe_delta_f64_batch(layer, h0[rows], gids[rows], gw[rows])
+    w64 = w_orc = w_cred = 0.0
+    for i in range(len(rows)):
+        sl = np.spacing(np.abs(got[rows[i]])).astype(np.float64)
+        w64 = max(w64, rel_err(d_got[i], x64[i], slack=sl)[0])
+        w_orc = max(w_orc, rel_err(d_ref[i], x64[i], slack=np.spacing(np.abs(ref[i])).astype(np.float64))[0])
+        w_cred = max(w_cred, rel_err(d_got[i], d_ref[i], slack=slack[i] + np.abs(d_ref[i] - x64[i]))[0])
+    print(f"prefill vs fp64: gpu {w64:.2e}, oracle {w_orc:.2e}; gpu vs oracle beyond the oracle's own "
+          f"rounding {w_cred:.2e}")
+    assert w64 <= F64_TOL
+    return w_cred
 
 
 def test_prefill_tiny_shapes(ctx, oracle):
@@ -128,8 +158,8 @@ def test_prefill_30b_64_tokens(ctx, oracle):
 
 def test_prefill_30b_512_tokens(ctx, oracle):
     """Config 4: 512 tokens through one 30B layer.  Every token's ids are
-    checked against the oracle's router + top-k; the hidden update on a sample
-    of 24 tokens spread over the batch (tokens are independent)."""
+    checked against the oracle's router + top-k, and every token's hidden
+    update against the oracle's whole layer."""
     layer = Layer(ctx, 2048, 128, 8, 768, layer_id=4)
     T = 512
     h0, got, gids, gw, _ = run_prefill(ctx, layer, T, index0=1000)
@@ -139,8 +169,7 @@ def test_prefill_30b_512_tokens(ctx, oracle):
         rid, rw = oracle.top_k(logits, layer.K, True)
         assert (gids[t] == rid).all(), t
         assert np.allclose(gw[t], rw, rtol=1e-5, atol=1e-7)
-    rows = np.linspace(0, T - 1, 24).astype(int)
-    assert check_against_oracle(oracle, layer, h0, got, gids, gw, rows=rows) <= TOL
+    assert check_against_oracle(oracle, layer, h0, got, gids, gw) <= TOL
 
 
 def test_prefill_235b_shape(ctx, oracle):
@@ -152,7 +181,9 @@ def test_prefill_235b_shape(ctx, oracle):
 def test_prefill_235b_512_tokens(ctx, oracle):
     """512 tokens through one 235B-shaped layer (D=4096, I=1536): about 32
     pairs per expert, so the grouped GEMM runs its 32- and 48-pair pass widths
-    over 64 groups.  Every token's ids exact; the hidden update on 8 tokens."""
+    over 64 groups.  Every token's ids exact; the hidden update on 64 tokens
+    spread over the batch (tokens are independent inside the block) against
+    the oracle and an fp64 evaluation (check_against_oracle, exact=True)."""
     layer = Layer(ctx, 4096, 128, 8, 1536, layer_id=13)
     T = 512
     h0, got, gids, gw, _ = run_prefill(ctx, layer, T, index0=2000)
@@ -162,8 +193,35 @@ def test_prefill_235b_512_tokens(ctx, oracle):
         rid, rw = oracle.top_k(logits, layer.K, True)
         assert (gids[t] == rid).all(), t
         assert np.allclose(gw[t], rw, rtol=1e-5, atol=1e-7)
-    rows = np.linspace(0, T - 1, 8).astype(int)
-    assert check_against_oracle(oracle, layer, h0, got, gids, gw, rows=rows) <= TOL
+    rows = np.linspace(0, T - 1, 64).astype(int)
+    assert check_against_oracle(oracle, layer, h0, got, gids, gw, rows=rows, exact=True) <= TOL
+
+
+def test_batched_235b_zipf_64_tokens(ctx, oracle):
+    """Config 5: 64 concurrent tokens through one 235B-shaped layer (D=4096,
+    E=128, k=8, I=1536) with the Zipf s=1.1 router of bench.py's batched
+    workload (the same generator, seed and layer 0).  The skew puts nearly
+    every token on the most popular experts, so the grouped GEMMs run their
+    64-pair pass at k_dim 4096 and 1536 beside experts with 0-2 pairs (the
+    reference's token-batch FFN plus its per-token fallback,
+    prefill.cpp:339-417, metal_bridge.mm:544-634).  All 64 tokens: ids
+    bit-exact, hidden update within 5e-4 of an fp64 evaluation and within
+    1e-3 of the oracle beyond the oracle's own rounding (check_against_oracle)."""
+    from smoe_amd import synthetic
+    D, E, K, I, T = 4096, 128, 8, 1536, 64
+    layer = Layer(ctx, D, E, K, I, layer_id=0, host=False)
+    u = synthetic.zipf_direction(D)
+    synthetic.zipf_bias_router(layer.router, u, D, E, 0, 1.1)
+    layer.host_copies()
+    h = hidden_states(ctx, T, D, index0=0)
+    synthetic.zipf_hidden(h, u)
+    h0, got, gids, gw, _ = run_prefill(ctx, layer, T, h=h)
+    counts = np.bincount(gids.ravel().astype(np.int64), minlength=E)
+    print(f"zipf: {int((counts > 0).sum())} experts touched, busiest {int(counts.max())} pairs, "
+          f"{int(((counts > 0) & (counts <= 2)).sum())} with 1-2 pairs")
+    assert counts.max() >= 49            # the 64-wide pass of the grouped GEMM runs
+    assert ((counts > 0) & (counts <= 2)).sum() >= 8
+    assert check_against_oracle(oracle, layer, h0, got, gids, gw, exact=True) <= TOL
 
 
 def test_prefill_235b_against_fp64(ctx):

@@ -63,8 +63,9 @@ def test_stack_single_layer_vs_oracle(ctx, oracle, engine, D, E, K, I, norm):
         assert check_layer(oracle, layer, h0, hid.cpu().numpy(), gids[0], gw[0]) <= TOL
 
 
-@pytest.mark.skip(reason="the stack kernel's d_model > 2048 variant faulted once on MI355X (memory aperture "
-                         "violation) with no cause found in its indexing; it is switched off and such shapes "
+@pytest.mark.skip(reason="the persistent kernel's d_model > 2048 variant is removed: it faulted once on MI355X "
+                         "(memory aperture violation) with no cause shown, and its combine stage staged only 16 "
+                         "rows per wave where d_model 4096 needs 32 (wrong values for half the rows); such shapes "
                          "take the per-layer path (test_stack_235b_shape_per_layer_path)")
 def test_stack_235b_layer(ctx, oracle):
     """Config 3 shape: one Qwen3-235B-A22B-shaped layer through the stack kernel."""

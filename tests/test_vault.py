@@ -81,7 +81,8 @@ def test_blobs_land_where_the_table_says(tmp_path):
 @pytest.mark.parametrize("case", [
     "truncated", "magic", "version3", "no_arch", "arch_magic", "activation", "top_k", "heads",
     "bits2", "group32", "misaligned", "past_eof", "packed_size", "tensor_type", "layout", "missing",
-    "duplicate", "layer_count", "table_overlaps_data", "d_model"])
+    "duplicate", "layer_count", "table_overlaps_data", "d_model", "packed_offset_wraps", "scales_offset_wraps",
+    "packed_misaligned", "scales_misaligned", "table_offset_wraps", "arch_offset_wraps"])
 def test_malformed_vaults_are_rejected(tmp_path, case):
     p = write(tmp_path)
     n = 2 * E
@@ -151,6 +152,26 @@ def test_malformed_vaults_are_rejected(tmp_path, case):
     elif case == "d_model":
         patch(p, 48, "<I", 2 * D)
         code, text = smoe_amd.SMOE_ERR_SHAPE, "d_model"
+    elif case == "packed_offset_wraps":
+        # offset + size wraps around 2^64 to a value inside the blob
+        patch(p, desc(0, 0) + 12, "<Q", (1 << 64) - 16)
+        text = "does not describe"
+    elif case == "scales_offset_wraps":
+        patch(p, desc(0, 1) + 28, "<Q", (1 << 64) - 2)
+        text = "does not describe"
+    elif case == "packed_misaligned":
+        patch(p, desc(0, 0) + 12, "<Q", 8)            # inside the blob, not 16-byte aligned
+        text = "not aligned"
+    elif case == "scales_misaligned":
+        patch(p, desc(0, 2) + 28, "<Q", smoe_amd.blob_layout(D, I)[0][5] - 1)
+        text = "not aligned"
+    elif case == "table_offset_wraps":
+        patch(p, 24, "<Q", (1 << 64) - 64)
+        text = "does not fit"
+    elif case == "arch_offset_wraps":
+        # the arch-block offset is 32-bit: largest value, past the data offset
+        patch(p, 60, "<I", 0xFFFFFFFF)
+        text = "arch-block offset"
     expect_error(p, code, text)
 
 
