@@ -404,6 +404,29 @@ int smoe_hip_vault_layer(const SmoeVault* vault, uint32_t moe_index, const void*
 int smoe_hip_vault_load(const SmoeVault* vault, void* dev_pool, uint64_t pool_bytes, void* hip_stream);
 const char* smoe_hip_vault_error(void);
 
+/* ---- allocation-free single-token decode ----------------------------------
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The same computation and kernels as
+ * smoe_hip_moe_decode with n_tokens = 1 (bit-identical results), with no
+ * context: every buffer the kernels need beyond the caller's is a fixed
+ * file-scope device array in the library (about 0.6 MB per GPU, held until
+ * the process ends), so the call allocates nothing and can be captured.
+ *   - shape limits: d_model <= 4096, d_ff <= 2048, n_experts <= 512,
+ *     top_k <= 16; larger shapes return SMOE_ERR_CAPACITY (message on stderr);
+ *   - set-up: smoe_metal_init sets the array up on its device; otherwise the
+ *     first call on a device must run outside stream capture
+ *     (SMOE_ERR_CAPTURE if not);
+ *   - hidden [d_model] fp32, device, updated in place; ids_out / weights_out
+ *     [top_k] and err_out [1] are optional device pointers (NULL: the
+ *     scratch's own); err_out receives the device-side flags OR-ed in
+ *     (bit 0: an exchange timed out);
+ *   - all calls on one GPU share its array: calls that overlap on one GPU
+ *     (e.g. on two streams without ordering) race.  Sequential calls are safe;
+ *     the array keeps the last call's contents. */
+int smoe_hip_moe_decode_static(const SmoeMoeShape* shape, const SmoeMoeLayer* layer, float* hidden,
+                               uint32_t* ids_out, float* weights_out, uint32_t* err_out, void* hip_stream);
+
 /* ---- per-kernel timing (telemetry; cf. the reference's --instrument buckets,
  * decode.hpp:36-74, and smoe_metal_kernel_dispatches) ------------------------
  * When enabled, every kernel the context launches outside graph capture is

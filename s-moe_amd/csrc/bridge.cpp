@@ -16,10 +16,14 @@
 #include <vector>
 
 #include "kernels.hpp"
+#include "shape.hpp"
 
 using smoe::ExpertPtrs;
 using smoe::LayerDesc;
 using smoe::MoeDims;
+using smoe::dims_of;
+using smoe::layer_of;
+using smoe::shape_check;
 
 namespace {
 
@@ -184,43 +188,6 @@ bool ref_shape_ok(const SmoeMetalCtx* ctx, uint32_t gate_rows, uint32_t gate_col
     if (gate_cols > SMOE_MAX_DIM || gate_rows > SMOE_MAX_DIM) return false;
     if (ctx && (gate_rows > ctx->max_rows || down_rows > ctx->max_rows)) return false;
     return true;
-}
-
-int shape_check(const SmoeMoeShape* s)
-{
-    if (!s) return SMOE_ERR_ARG;
-    if (s->bits != 4) return SMOE_ERR_BITS;
-    const uint32_t g = s->group_size;
-    if (g == 0 || g % 32 != 0 || g > 128 || (g & (g - 1))) return SMOE_ERR_SHAPE;
-    if (s->d_model == 0 || s->d_ff == 0 || s->n_experts == 0 || s->top_k == 0) return SMOE_ERR_SHAPE;
-    if (s->d_model % 64 || s->d_ff % 64 || s->d_model % g || s->d_ff % g) return SMOE_ERR_SHAPE;
-    if (s->d_model > SMOE_MAX_DIM || s->d_ff > SMOE_MAX_DIM) return SMOE_ERR_SHAPE;
-    if (g != 64) return SMOE_ERR_SHAPE;   // the vault format's group (shatter_moe.py Q2_GROUP_SIZE)
-    if (s->top_k > SMOE_MAX_ACTIVE || s->top_k > s->n_experts) return SMOE_ERR_SHAPE;
-    if (s->n_experts > SMOE_MAX_EXPERTS) return SMOE_ERR_SHAPE;
-    if (static_cast<uint64_t>(s->top_k) * (s->d_ff / 32) > 8ull * 64 * 4) return SMOE_ERR_SHAPE;
-    return SMOE_OK;
-}
-
-MoeDims dims_of(const SmoeMoeShape* s)
-{
-    return MoeDims{s->d_model, s->n_experts, s->top_k, s->d_ff, s->group_size, s->norm_topk ? 1u : 0u};
-}
-
-LayerDesc layer_of(const SmoeMoeLayer* L)
-{
-    LayerDesc d;
-    d.norm_w = L->norm_w;
-    d.router_w = L->router_w;
-    d.experts = L->experts;
-    d.stride = L->expert_stride;
-    d.off[0] = L->gate_packed_offset;
-    d.off[1] = L->gate_scales_offset;
-    d.off[2] = L->up_packed_offset;
-    d.off[3] = L->up_scales_offset;
-    d.off[4] = L->down_packed_offset;
-    d.off[5] = L->down_scales_offset;
-    return d;
 }
 
 bool stream_capturing(hipStream_t s)
@@ -423,6 +390,9 @@ extern "C" SmoeMetalCtx* smoe_metal_init(size_t slot_bytes)
         return nullptr;
     }
     ctx->stream = ctx->own_stream;
+    // the allocation-free decode entry point's per-device scratch (its address
+    // and first clearing), here so that later calls need no set-up
+    (void)smoe::static_scratch_setup();
     return ctx;
 }
 

@@ -206,6 +206,11 @@ hipError_t launch_grouped_down(const MoeDims& d, const LayerDesc& L, const uint3
 hipError_t launch_combine_pairs(const float* y, const float* w, uint32_t T, uint32_t K, uint32_t D, float* hidden,
                                 hipStream_t s);
 
+// ---- static scratch of smoe_hip_moe_decode_static (decode_static.hip) -----
+// Takes the current device's address of the file-scope scratch array and
+// clears it, once per device (synchronous; outside stream capture).
+uint64_t* static_scratch_setup();
+
 // ---- measurement (probe.hip) ----------------------------------------------
 // Streams `bytes` (a multiple of 16) from src with non-temporal 128-bit loads;
 // folds what it read into *sink.

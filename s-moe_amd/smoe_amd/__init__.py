@@ -129,6 +129,8 @@ SIGNATURES = [
     ("smoe_hip_profile_read", _I, [_VP, _U32, C.POINTER(C.c_uint64), C.POINTER(C.c_double)]),
     ("smoe_hip_last_error", C.c_char_p, [_VP]),
     ("smoe_hip_stream_read", _I, [_VP, _VP, _U64, _VP]),
+    ("smoe_hip_moe_decode_static", _I, [C.POINTER(SmoeMoeShape), C.POINTER(SmoeMoeLayer), _VP, _VP, _VP, _VP,
+                                        _VP]),
 ]
 
 KERNEL_MOE_UP, KERNEL_GATE_UP, KERNEL_MOE_DOWN, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
