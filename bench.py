@@ -39,7 +39,7 @@ CONFIGS = {
 HBM_PEAK_GBS = 8000.0
 SEED = 20261201
 KERNEL_SYMBOLS = {"moe_up": "k_moe_up", "moe_down": "k_down_combine", "decode_stack": "k_decode_stack",
-                  "moe_layer": "k_moe_layer"}
+                  "moe_layer": "k_moe_layer", "decode_spec": "k_decode_spec"}
 
 
 def log(msg):
@@ -55,6 +55,7 @@ def kernel_bytes(c):
     mat = D * I // 2 + D * I // 64 * 2            # packed nibbles + fp16 scales of one matrix
     return {
         "decode_stack": c["layers"] * (K * 3 * mat + 2 * E * D + 12 * D),
+        "decode_spec": c["layers"] * (K * 3 * mat + 2 * E * D + 12 * D),
         # the whole block: router bf16 + norm weights + 8 experts' gate/up/down + hidden in and out
         "moe_layer": K * 3 * mat + 2 * E * D + 2 * D + 8 * D,
         # router bf16 + norm weights + hidden in + 8 experts' gate+up + h out
@@ -94,10 +95,12 @@ def main():
     ap.add_argument("--replicas", type=int, default=4, help="prefill/batched: layer replicas rotated")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (0: config's)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
-    ap.add_argument("--engine", default="stack", choices=("stack", "split", "persistent", "layers"),
+    ap.add_argument("--engine", default="stack", choices=("stack", "split", "persistent", "prefetch", "layers"),
                     help="stack: smoe_hip_moe_decode_stack, per-layer launches (one per layer where the shape "
                          "allows); split: the same with two launches per layer; persistent: the whole step in "
-                         "one persistent launch; layers: one smoe_hip_moe_decode call per layer")
+                         "one persistent launch; prefetch: the whole step in one persistent launch that "
+                         "prefetches the next layer's predicted experts into LDS; layers: one "
+                         "smoe_hip_moe_decode call per layer")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU work the baseline sample aims at")
     ap.add_argument("--profile-steps", type=int, default=8, help="replays of the event-timed step (0: skip)")
@@ -178,9 +181,9 @@ def main():
     torch.cuda.synchronize()
     layer_arr = (smoe_amd.SmoeMoeLayer * NL)(*layers)
 
-    ctx.set_decode_engine({"persistent": smoe_amd.DECODE_PERSISTENT,
+    ctx.set_decode_engine({"persistent": smoe_amd.DECODE_PERSISTENT, "prefetch": smoe_amd.DECODE_PREFETCH,
                            "split": smoe_amd.DECODE_SPLIT}.get(args.engine, smoe_amd.DECODE_LAUNCHES))
-    if args.engine in ("stack", "split", "persistent"):
+    if args.engine in ("stack", "split", "persistent", "prefetch"):
 
         def step():
             ctx.moe_decode_stack(shape, layer_arr, hidden.data_ptr())
@@ -237,6 +240,8 @@ def main():
                    "engine": {"stack": "stack API, per-layer launches",
                               "split": "stack API, two launches per layer",
                               "persistent": "stack API, one persistent launch per step",
+                              "prefetch": "stack API, one persistent launch per step, next layer's predicted "
+                                          "experts prefetched to LDS",
                               "layers": "one decode call per layer"}[args.engine],
                    "resident_expert_bytes": NL * E * raw},
     }
@@ -319,7 +324,8 @@ def stream_ceiling(ctx, torch, pool, launches=6):
 def _read_profile(ctx, smoe_amd):
     out = {}
     for kid, name in ((smoe_amd.KERNEL_MOE_UP, "moe_up"), (smoe_amd.KERNEL_MOE_DOWN, "moe_down"),
-                      (smoe_amd.KERNEL_STACK, "decode_stack"), (smoe_amd.KERNEL_MOE_LAYER, "moe_layer")):
+                      (smoe_amd.KERNEL_STACK, "decode_stack"), (smoe_amd.KERNEL_MOE_LAYER, "moe_layer"),
+                      (smoe_amd.KERNEL_STACK_PREFETCH, "decode_spec")):
         n, ms = ctx.profile_read(kid)
         if n:
             out[name] = (n, ms * 1e3 / n)
@@ -384,7 +390,7 @@ def cpu_baseline(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, targ
             gpu_h.copy_(torch.from_numpy(h))
             lay = smoe_amd.make_layer(norm_w.data_ptr(), router[l].data_ptr(),
                                       pool.data_ptr() + l * layer_bytes, stride, off)
-            if engine == "persistent":
+            if engine in ("persistent", "prefetch"):
                 ctx.moe_decode_stack(shape, [lay], gpu_h.data_ptr(), ids.data_ptr())
             else:
                 ctx.moe_decode(shape, lay, gpu_h.data_ptr(), 1, ids.data_ptr())

@@ -256,7 +256,17 @@ int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
  *     fp32 summation order.  Its layer table is copied to the device when it
  *     differs from the previous call's (outside graph capture; under capture
  *     a new table gives SMOE_ERR_CAPTURE).  Shapes it does not cover
- *     (d_model > 2048, d_ff > 2048, more than 512 experts) take the launches. */
+ *     (d_model > 2048, d_ff > 2048, more than 512 experts) take the launches.
+ *   SMOE_DECODE_PREFETCH: one persistent launch per step as above, in which
+ *     every CU copies its slice of the next layer's predicted experts (layer
+ *     l + 1's router applied to layer l's input) into LDS while layer l runs;
+ *     a mispredicted slice is fetched when the layer's exact top-k is known.
+ *     The prediction changes only where weights come from, not results.
+ *     Shapes: d_model 2048, top_k 8, 8..128 experts, d_ff a multiple of 192
+ *     up to 768 (Qwen3-30B-A3B), on a device with 256 CUs; others take the
+ *     launches.  Table handling as SMOE_DECODE_PERSISTENT.  Opt-in: at the
+ *     30B shape it is currently slower per layer than SMOE_DECODE_LAUNCHES
+ *     (copies in flight on a CU lengthen its exchange waits). */
 int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
                               const SmoeMoeLayer* layers, uint32_t n_layers, float* hidden,
                               uint32_t* ids_out, float* weights_out);
@@ -264,6 +274,7 @@ int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
 #define SMOE_DECODE_LAUNCHES   0
 #define SMOE_DECODE_PERSISTENT 1
 #define SMOE_DECODE_SPLIT      2
+#define SMOE_DECODE_PREFETCH   3
 /* Select the engine of smoe_hip_moe_decode_stack (and, for SMOE_DECODE_SPLIT,
  * the form of smoe_hip_moe_decode) for this context. */
 int smoe_hip_set_decode_engine(SmoeMetalCtx* ctx, int engine);
@@ -448,7 +459,8 @@ int smoe_hip_moe_decode_static(const SmoeMoeShape* shape, const SmoeMoeLayer* la
 #define SMOE_KERNEL_GEMV         13   /* dense trunk: grouped bf16 GEMV                          */
 #define SMOE_KERNEL_ATTENTION    14   /* dense trunk: QK norm/RoPE/KV append + decode attention   */
 #define SMOE_KERNEL_STREAM       15   /* measurement: streaming-read ceiling (smoe_hip_stream_read) */
-#define SMOE_KERNEL_KINDS        16
+#define SMOE_KERNEL_STACK_PREFETCH 16 /* decode: every layer in one launch, predicted experts prefetched to LDS */
+#define SMOE_KERNEL_KINDS        20
 int smoe_hip_profile_enable(SmoeMetalCtx* ctx, int enable);
 int smoe_hip_profile_read(SmoeMetalCtx* ctx, uint32_t kernel, uint64_t* launches, double* total_ms);
 

@@ -732,7 +732,8 @@ extern "C" int smoe_hip_stream_read(SmoeMetalCtx* ctx, const void* src, uint64_t
 
 extern "C" int smoe_hip_set_decode_engine(SmoeMetalCtx* ctx, int engine)
 {
-    if (!ctx || (engine != SMOE_DECODE_LAUNCHES && engine != SMOE_DECODE_PERSISTENT && engine != SMOE_DECODE_SPLIT))
+    if (!ctx || (engine != SMOE_DECODE_LAUNCHES && engine != SMOE_DECODE_PERSISTENT && engine != SMOE_DECODE_SPLIT &&
+                 engine != SMOE_DECODE_PREFETCH))
         return SMOE_ERR_ARG;
     ctx->decode_engine = engine;
     return SMOE_OK;
@@ -799,7 +800,8 @@ extern "C" int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* 
     int rc = shape_check(shape);
     if (rc != SMOE_OK) return rc;
     const MoeDims d = dims_of(shape);
-    if (ctx->decode_engine != SMOE_DECODE_PERSISTENT || !smoe::stack_supported(d)) {
+    const bool spec = ctx->decode_engine == SMOE_DECODE_PREFETCH && smoe::spec_supported(d);
+    if (!spec && (ctx->decode_engine != SMOE_DECODE_PERSISTENT || !smoe::stack_supported(d))) {
         // two launches per layer
         for (uint32_t l = 0; l < n_layers; ++l) {
             rc = moe_forward(ctx, shape, &layers[l], hidden, 1, ids_out ? ids_out + size_t(l) * d.K : nullptr,
@@ -811,7 +813,8 @@ extern "C" int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* 
     StackScratch& s = ctx->ss;
     const bool capturing = stream_capturing(ctx->stream);
     // exchange words: grown (and zeroed) outside capture only
-    const size_t words = smoe::stack_xch_words(d, std::min<uint32_t>(n_layers, smoe::ST_MAX_LAYERS));
+    const uint32_t nl = std::min<uint32_t>(n_layers, smoe::ST_MAX_LAYERS);
+    const size_t words = spec ? smoe::spec_xch_words(d, nl) : smoe::stack_xch_words(d, nl);
     if (!s.ctl || s.words < words) {
         if (capturing) return SMOE_ERR_CAPTURE;
         if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
@@ -852,13 +855,17 @@ extern "C" int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* 
     // one launch per ST_MAX_LAYERS layers (the kernel keeps its layer table in LDS)
     for (uint32_t l0 = 0; l0 < n_layers; l0 += smoe::ST_MAX_LAYERS) {
         const uint32_t n = std::min<uint32_t>(smoe::ST_MAX_LAYERS, n_layers - l0);
-        if (!timed(ctx, SMOE_KERNEL_STACK, "decode_stack", [&] {
-                return smoe::launch_decode_stack(d, s.tbl + l0, n, hidden, s.xch, s.ctl,
-                                                 ids_out ? ids_out + size_t(l0) * d.K : nullptr,
-                                                 weights_out ? weights_out + size_t(l0) * d.K : nullptr,
-                                                 ctx->d_err, ctx->stream);
-            }))
-            return SMOE_ERR_HIP;
+        uint32_t* ids = ids_out ? ids_out + size_t(l0) * d.K : nullptr;
+        float* w = weights_out ? weights_out + size_t(l0) * d.K : nullptr;
+        const bool ok = spec ? timed(ctx, SMOE_KERNEL_STACK_PREFETCH, "decode_spec", [&] {
+                                   return smoe::launch_decode_spec(d, s.tbl + l0, n, hidden, s.xch, s.ctl, ids, w,
+                                                                   ctx->d_err, nullptr, ctx->stream);
+                               })
+                             : timed(ctx, SMOE_KERNEL_STACK, "decode_stack", [&] {
+                                   return smoe::launch_decode_stack(d, s.tbl + l0, n, hidden, s.xch, s.ctl, ids, w,
+                                                                    ctx->d_err, ctx->stream);
+                               });
+        if (!ok) return SMOE_ERR_HIP;
     }
     ctx->dispatches.fetch_add(uint64_t(n_layers) * d.K, std::memory_order_relaxed);
     return SMOE_OK;

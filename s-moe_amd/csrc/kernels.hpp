@@ -132,6 +132,19 @@ size_t stack_xch_words(const MoeDims& d, uint32_t n_layers);
 hipError_t launch_decode_stack(const MoeDims& d, const LayerDesc* layers, uint32_t n_layers, float* hidden,
                                uint64_t* xch, uint32_t* ctl, uint32_t* ids, float* w, uint32_t* err, hipStream_t s);
 
+// ---- decode, whole stack in one persistent launch with LDS prefetch of the
+// predicted experts (moe_spec.hip) ---------------------------------------------
+// d_model 2048, top-k 8, n_experts 8..128, d_ff a multiple of 192 up to 768;
+// 256 blocks of 12 waves, one per CU (the device must have exactly 256 CUs).
+bool spec_supported(const MoeDims& d);
+size_t spec_xch_words(const MoeDims& d, uint32_t n_layers);
+// as launch_decode_stack; trace (optional) receives 16 words per (layer,
+// block): phase timestamps of compute wave 0 (s_memrealtime) and, in word 15,
+// hits << 32 | hit << 16 | slot expert
+hipError_t launch_decode_spec(const MoeDims& d, const LayerDesc* layers, uint32_t n_layers, float* hidden,
+                              uint64_t* xch, uint32_t* ctl, uint32_t* ids, float* w, uint32_t* err, uint64_t* trace,
+                              hipStream_t s);
+
 // out [rows] = W [rows x cols] bf16 . x [cols] (reference-surface dense GEMV)
 hipError_t launch_matvec_bf16(const uint16_t* W, const float* x, float* out, uint32_t rows, uint32_t cols,
                               hipStream_t s);

@@ -258,6 +258,70 @@ __device__ __forceinline__ void merge8(uint32_t (&a)[8])
     for (int i = 0; i < 8; ++i) a[i] = h[i];
 }
 
+// The top 8 of the 128 keys held two per lane (k0, k1), sorted in descending
+// order, in every lane's c[0..7] (the network described above).
+__device__ __forceinline__ void net_top8(uint32_t k0, uint32_t k1, uint32_t (&c)[8])
+{
+    // lane bit 5: 2 + 2 keys
+    uint32_t a0 = max(k0, k1), a1 = min(k0, k1);
+    {
+        uint32_t x0, y0, x1, y1;
+        swap_pair<5>(a0, x0, y0);
+        swap_pair<5>(a1, x1, y1);
+        c[0] = max(x0, y0);
+        uint32_t mid0 = min(x0, y0), mid1 = max(x1, y1);
+        c[3] = min(x1, y1);
+        cmp_swap(mid1, mid0);
+        c[1] = mid1;
+        c[2] = mid0;
+    }
+    // lane bit 4: 4 + 4 keys, odd-even merge (evens, odds, then neighbours)
+    {
+        uint32_t x[4], y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) swap_pair<4>(c[i], x[i], y[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cmp_swap(x[i], y[i]);   // x = max, y = min of index i
+        // evens: {x0, y0} merged with {x2, y2}
+        uint32_t e0 = x[0], e1 = y[0], e2 = x[2], e3 = y[2];
+        cmp_swap(e1, e2);
+        // odds: {x1, y1} merged with {x3, y3}
+        uint32_t o0 = x[1], o1 = y[1], o2 = x[3], o3 = y[3];
+        cmp_swap(o1, o2);
+        c[0] = e0;
+        c[7] = o3;
+        cmp_swap(o0, e1);
+        cmp_swap(o1, e2);
+        cmp_swap(o2, e3);
+        c[1] = o0; c[2] = e1; c[3] = o1; c[4] = e2; c[5] = o2; c[6] = e3;
+    }
+    merge8<DPP_ROW_ROR8>(c);
+    merge8<DPP_ROW_HALF_MIRROR>(c);
+    merge8<DPP_QUAD_XOR2>(c);
+    merge8<DPP_QUAD_XOR1>(c);
+}
+
+// Positions of the 8 largest of n <= 128 scores (two per lane, position
+// lane + 64 j), largest first, ties to the lower position: lane r < 8 returns
+// the position of rank r.  Scores are compared by their order-preserving
+// bits (the low 7 replaced by the position, as in topk_net), so scores equal
+// in their top 25 bits rank by position; a non-finite score still yields a
+// position below n.  Used where an exact top-k is not needed.
+__device__ __forceinline__ uint32_t top8_positions(const float (&v)[2], uint32_t n)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    uint32_t key[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t pos = lane + WAVE * j;
+        key[j] = pos < n ? ((order_bits(v[j]) & ~127u) | (127u - pos)) : 0u;
+    }
+    uint32_t c[8];
+    net_top8(key[0], key[1], c);
+    const uint32_t pos = 127u - (sorted_at(c, static_cast<uint32_t>(lane) & 7u) & 127u);
+    return min(pos, n - 1);
+}
+
 template <int VPL>
 __device__ uint32_t topk_net(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t norm, uint32_t& my_id, float& my_w,
                              uint2* slots)
@@ -291,44 +355,8 @@ __device__ uint32_t topk_net(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t n
         sum = wave_sum(sum);
         const float inv_sum = (sum > 0.f) ? 1.0f / sum : 0.f;
 
-        // lane bit 5: 2 + 2 keys
-        uint32_t a0 = max(key[0], key[1]), a1 = min(key[0], key[1]);
         uint32_t c[8];
-        {
-            uint32_t x0, y0, x1, y1;
-            swap_pair<5>(a0, x0, y0);
-            swap_pair<5>(a1, x1, y1);
-            c[0] = max(x0, y0);
-            uint32_t mid0 = min(x0, y0), mid1 = max(x1, y1);
-            c[3] = min(x1, y1);
-            cmp_swap(mid1, mid0);
-            c[1] = mid1;
-            c[2] = mid0;
-        }
-        // lane bit 4: 4 + 4 keys, odd-even merge (evens, odds, then neighbours)
-        {
-            uint32_t x[4], y[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) swap_pair<4>(c[i], x[i], y[i]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) cmp_swap(x[i], y[i]);   // x = max, y = min of index i
-            // evens: {x0, y0} merged with {x2, y2}
-            uint32_t e0 = x[0], e1 = y[0], e2 = x[2], e3 = y[2];
-            cmp_swap(e1, e2);
-            // odds: {x1, y1} merged with {x3, y3}
-            uint32_t o0 = x[1], o1 = y[1], o2 = x[3], o3 = y[3];
-            cmp_swap(o1, o2);
-            c[0] = e0;
-            c[7] = o3;
-            cmp_swap(o0, e1);
-            cmp_swap(o1, e2);
-            cmp_swap(o2, e3);
-            c[1] = o0; c[2] = e1; c[3] = o1; c[4] = e2; c[5] = o2; c[6] = e3;
-        }
-        merge8<DPP_ROW_ROR8>(c);
-        merge8<DPP_ROW_HALF_MIRROR>(c);
-        merge8<DPP_QUAD_XOR2>(c);
-        merge8<DPP_QUAD_XOR1>(c);
+        net_top8(key[0], key[1], c);
 
         // probabilities: of every position, of the proposed ranks (lane r),
         // and the largest over the unselected positions
