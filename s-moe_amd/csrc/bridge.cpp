@@ -761,7 +761,7 @@ static int moe_forward(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, const SmoeM
     const LayerDesc L = layer_of(layer);
     uint32_t* ids = ids_out ? ids_out : s.ids;
     float* w = weights_out ? weights_out : s.w;
-    if (n_tokens == 1 && ctx->decode_engine != SMOE_DECODE_SPLIT && smoe::layer_supported(d)) {
+    if (n_tokens == 1 && ctx->decode_engine != SMOE_DECODE_SPLIT && smoe::layer_supported(d, L)) {
         if (!timed(ctx, SMOE_KERNEL_MOE_LAYER, "moe_layer", [&] {
                 return smoe::launch_moe_layer(d, L, hidden, s.lx, ids, w, ctx->d_err, ctx->stream);
             }))

@@ -99,8 +99,9 @@ __host__ __device__ constexpr size_t lx_words(uint32_t D, uint32_t E, uint32_t I
 {
     return LX_HEAD + 8ull * (lx_pad(E) + lx_pad(I) + lx_pad(D));
 }
-// true when k == 8 and the shape's grid fits on the device at once
-bool layer_supported(const MoeDims& d);
+// true when k == 8, the shape's grid fits on the device at once and the
+// layer's tensors are 16-byte aligned
+bool layer_supported(const MoeDims& d, const LayerDesc& L);
 // the whole MoE block of one token: hidden [D] += MoE(RMSNorm(hidden));
 // ids/w [K] receive the routing; err bit 0 reports an exchange time-out
 hipError_t launch_moe_layer(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx, uint32_t* ids,

@@ -11,7 +11,11 @@
 //      rows t, t + n, ... (common.hpp:293-306), published as flag-carrying
 //      words in XCD x's logit copy;
 //   2. softmax + top-k (scout.cpp:77-123) + renormalisation
-//      (decode.cpp:296-302) from that copy, in every wave;
+//      (decode.cpp:296-302) from that copy, in every wave; where registers
+//      allow, the gate/up rows of the expert the top-k network proposes for
+//      rank x are requested before the softmax and the exact check finish
+//      (requested again, for the selected expert, should the check overturn
+//      the proposal);
 //   3. t < n_up: RB rows (8, or 6 where that fills every wave) of gate and
 //      up of expert ids[x] and
 //      h = silu(gate) * up (kernels.metal:240-337), published in XCD x's
@@ -84,7 +88,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
     constexpr int NG = WAVE / GL;      // down groups per wave
     constexpr int RW = NG * DR;        // down rows per wave
     constexpr int SH = SEG - ilog2(DR);
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & (WAVE - 1);
     const uint32_t D = d.D, nch = D >> 5;
     const uint32_t nbx = gridDim.x >> 3;
     const uint32_t t = blockIdx.x >> 3;
@@ -97,6 +101,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
     uint64_t* py = lx + LX_HEAD + 8u * lx_pad(d.E) + 8u * lx_pad(d.I);
     const uint32_t py_stride = lx_pad(D);
     bool timed_out = false;
+
 
     // 1. hidden, norm weight and router rows t, t + nbx
     const bool producer = t < d.E;
@@ -222,48 +227,49 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
     uint32_t my_id;
     float my_w;
     __shared__ uint2 slots[TOPK_SLOTS];
-    topk_latency<VPL>(v, d.E, d.K, d.norm_topk, my_id, my_w, slots);
-    // (clamped: a timed-out exchange must still index inside the pool)
-    const uint32_t expert = min(readlane_u32(my_id, static_cast<int>(x)), d.E - 1);
-    if (x == 0 && t == 0 && static_cast<uint32_t>(lane) < d.K) {
-        ids_out[lane] = my_id;
-        w_out[lane] = my_w;
+    // Where the gate/up rows in flight leave registers for the rest of the
+    // top-k: the expert of rank x as the top-k network proposes it (E <= 128),
+    // so its weights are requested while the softmax and the check run.
+    // Otherwise (more experts, or wide rows) the exact top-k first.
+    constexpr bool PROPOSE = VPL == 2 && RB * CPL * 2 * 4 <= 64;
+    uint32_t prop, expert;
+    NetTopk net;
+    if constexpr (PROPOSE) {
+        topk_net_begin(v, d.E, net);
+        prop = __builtin_amdgcn_readfirstlane(topk_net_rank(net, x, d.E));
+    } else {
+        topk_latency<VPL>(v, d.E, d.K, d.norm_topk, my_id, my_w, slots);
+        prop = min(readlane_u32(my_id, static_cast<int>(x)), d.E - 1);
     }
-    const uint8_t* blob = L.experts + static_cast<size_t>(expert) * L.stride;
 
-    // down rows of rank x: lane (group gi, chunk c) owns chunk c of rows
-    // rowb .. rowb + DR - 1
+    // gate/up rows RB t .. RB t + RB - 1 and down rows of rank x: lane
+    // (group gi, chunk c) owns chunk c of down rows rowb .. rowb + DR - 1
+    const uint32_t rowg = t * RB;
+    const uint32_t row_bytes = D >> 1, row_scales = D / LX_GROUP;
     const uint32_t CH = d.I >> 5;
     const int gi = lane >> SEG, c0 = lane & (GL - 1);
     const bool act = static_cast<uint32_t>(c0) < CH;
     const uint32_t dc = act ? static_cast<uint32_t>(c0) : CH - 1;
     const uint32_t rowb = t * RW + gi * DR;
+    // The scales of the wave's rows are contiguous (RB * D / 32 bytes of
+    // gate, as many of up, RW * I / 32 of down): one 16-byte piece per lane
+    // (a load instruction costs the CU a request slot whatever its width),
+    // issued ahead of the rows and passed to the lanes that use them through
+    // LDS.  Host-checked: the pieces are 16-byte aligned and the gate/up
+    // ones fit one per lane.
+    constexpr uint32_t DN_MAX_I = SEG == 5 ? 1024u : 2048u;
+    constexpr int NSD = (RW * DN_MAX_I / 512 + WAVE - 1) / WAVE;   // down scale pieces per lane
+    const uint32_t nsq_up = RB * D / 512, nsq_dn = RW * d.I / 512;
+    uint4 va[RB][CPL], vb[RB][CPL], qa_s, qb_s, qd_s[NSD];
     uint4 dv[DR];
-    uint16_t dsv[DR];
-    auto issue_down = [&] {
-        const uint8_t* pdn = blob + L.off[4];
-        const uint16_t* sdn = reinterpret_cast<const uint16_t*>(blob + L.off[5]);
-        const uint32_t drow_bytes = d.I >> 1, drow_scales = d.I / LX_GROUP;
-#pragma unroll
-        for (int i = 0; i < DR; ++i) {
-            const size_t row = rowb + i;
-            dv[i] = load_stream_u4(pdn + row * drow_bytes + dc * 16);
-            dsv[i] = load_stream_u16(sdn + row * drow_scales + (dc * 32) / LX_GROUP);
-        }
-    };
-
-    // 3. gate/up rows RB t .. RB t + RB - 1 of rank x -> h.  (Issuing the down loads
-    //    any earlier than after this wave's up compute slows the launch:
-    //    they compete with the gate/up stream every wave waits for.)
-    if (t < n_up) {
-        const uint32_t rowg = t * RB;
+    __shared__ uint4 sc_up[2][WAVE];
+    __shared__ uint4 sc_dn[NSD * WAVE];
+    auto issue_up = [&](const uint8_t* blob) {
         const uint8_t* pa = blob + L.off[0];
-        const uint16_t* sa = reinterpret_cast<const uint16_t*>(blob + L.off[1]);
         const uint8_t* pb = blob + L.off[2];
-        const uint16_t* sb = reinterpret_cast<const uint16_t*>(blob + L.off[3]);
-        const uint32_t row_bytes = D >> 1, row_scales = D / LX_GROUP;
-        uint4 va[RB][CPL], vb[RB][CPL];
-        uint16_t sva[RB][CPL], svb[RB][CPL];
+        const uint32_t q = min(static_cast<uint32_t>(lane), nsq_up - 1);
+        qa_s = load_stream_u4(blob + L.off[1] + static_cast<size_t>(rowg) * row_scales * 2 + q * 16);
+        qb_s = load_stream_u4(blob + L.off[3] + static_cast<size_t>(rowg) * row_scales * 2 + q * 16);
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
             const size_t row = rowg + i;
@@ -272,11 +278,53 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
                 const uint32_t c = min(lane + WAVE * j, nch - 1);
                 va[i][j] = load_stream_u4(pa + row * row_bytes + c * 16);
                 vb[i][j] = load_stream_u4(pb + row * row_bytes + c * 16);
-                sva[i][j] = load_stream_u16(sa + row * row_scales + (c * 32) / LX_GROUP);
-                svb[i][j] = load_stream_u16(sb + row * row_scales + (c * 32) / LX_GROUP);
             }
         }
+    };
+    auto issue_down = [&](const uint8_t* blob) {
+        const uint8_t* pdn = blob + L.off[4];
+        const uint32_t drow_bytes = d.I >> 1;
+#pragma unroll
+        for (int k = 0; k < NSD; ++k) {
+            const uint32_t q = min(static_cast<uint32_t>(k * WAVE + lane), nsq_dn - 1);
+            qd_s[k] = load_stream_u4(blob + L.off[5] + static_cast<size_t>(t) * RW * (d.I / 32) + q * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < DR; ++i) {
+            const size_t row = rowb + i;
+            dv[i] = load_stream_u4(pdn + row * drow_bytes + dc * 16);
+        }
+    };
+    const uint8_t* blob;
+    if constexpr (PROPOSE) {
+        if (t < n_up) issue_up(L.experts + static_cast<size_t>(prop) * L.stride);
         __builtin_amdgcn_sched_barrier(0);
+        // the rest of the top-k while the rows land
+        topk_net_finish<VPL>(v, d.E, d.K, d.norm_topk, my_id, my_w, slots, net);
+        // (clamped: a timed-out exchange must still index inside the pool)
+        expert = min(readlane_u32(my_id, static_cast<int>(x)), d.E - 1);
+        blob = L.experts + static_cast<size_t>(expert) * L.stride;
+        // a proposal the exact selection overturned (ties, values equal
+        // after rounding): the rows again, of the selected expert
+        if (expert != prop && t < n_up) issue_up(blob);
+    } else {
+        expert = prop;
+        blob = L.experts + static_cast<size_t>(prop) * L.stride;
+    }
+    if (x == 0 && t == 0 && static_cast<uint32_t>(lane) < d.K) {
+        ids_out[lane] = my_id;
+        w_out[lane] = my_w;
+    }
+
+    // 3. gate/up rows of rank x -> h
+    if (t < n_up) {
+        if constexpr (!PROPOSE) issue_up(blob);
+        __builtin_amdgcn_sched_barrier(0);
+        sc_up[0][lane] = qa_s;
+        sc_up[1][lane] = qb_s;
+        __builtin_amdgcn_wave_barrier();
+        const uint16_t* sga = reinterpret_cast<const uint16_t*>(sc_up[0]);
+        const uint16_t* sgb = reinterpret_cast<const uint16_t*>(sc_up[1]);
         float part[NR];
 #pragma unroll
         for (int i = 2 * RB; i < NR; ++i) part[i] = 0.f;
@@ -285,8 +333,9 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
             float ga = 0.f, ua = 0.f;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
-                ga = fmaf(f16_bits_to_f32(sva[i][j]), q4_chunk_dot8(va[i][j], qa[j]), ga);
-                ua = fmaf(f16_bits_to_f32(svb[i][j]), q4_chunk_dot8(vb[i][j], qa[j]), ua);
+                const uint32_t si = i * row_scales + (min(lane + WAVE * j, nch - 1) * 32) / LX_GROUP;
+                ga = fmaf(f16_bits_to_f32(sga[si]), q4_chunk_dot8(va[i][j], qa[j]), ga);
+                ua = fmaf(f16_bits_to_f32(sgb[si]), q4_chunk_dot8(vb[i][j], qa[j]), ua);
             }
             part[2 * i] = ga;
             part[2 * i + 1] = ua;
@@ -302,11 +351,20 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
 
     // 4. down rows of rank x against all of h
     if (t < n_down) {
-        issue_down();
+        // (after h is published: a memory operation waits for the requests
+        // the CU has queued ahead of it, so a publication behind these rows
+        // would wait for them; issued with the gate/up rows, or once those
+        // have landed, they delay h by more than they save)
+        issue_down(blob);
         // all of this XCD's h, staged in LDS: passes of 16 words per lane,
         // every load of a pass in flight before any is checked (addresses
-        // past the end re-read word I - 1)
-        __shared__ __align__(16) float h_s[LX_MAX_I];
+        // past the end re-read word I - 1).  Quad-major: quad q (values 4q ..
+        // 4q + 3) of 32-value chunk c at float4 q * (CH + 1) + c, so the 64
+        // lanes reading quad q of their chunks touch consecutive addresses
+        // (the + 1 spreads the writes of a pass over the banks).
+        __shared__ __align__(16) float h_s[8 * (LX_MAX_I / 32 + 1) * 4];
+        const uint32_t chp = CH + 1;
+        auto hpos = [&](uint32_t k) { return (((k & 31u) >> 2) * chp + (k >> 5)) * 4u + (k & 3u); };
         {
             const uint32_t passes = (d.I + 16 * WAVE - 1) / (16 * WAVE);
             uint32_t spins = 0;
@@ -320,7 +378,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
                         w64[m] = get_agent(hxc + min(p * 16 * WAVE + lane + WAVE * m, d.I - 1));
 #pragma unroll
                     for (int m = 0; m < 16; ++m) {
-                        h_s[min(p * 16 * WAVE + lane + WAVE * m, d.I - 1)] =
+                        h_s[hpos(min(p * 16 * WAVE + lane + WAVE * m, d.I - 1))] =
                             __uint_as_float(static_cast<uint32_t>(w64[m]));
                         all &= static_cast<uint32_t>(w64[m] >> 32) == tag;
                     }
@@ -338,10 +396,10 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
         __builtin_amdgcn_wave_barrier();
         float hx[32];
         {
-            const float4* hp = reinterpret_cast<const float4*>(h_s + dc * 32);
+            const float4* hp = reinterpret_cast<const float4*>(h_s);
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                const float4 f = hp[q];
+                const float4 f = hp[q * chp + dc];
                 hx[4 * q + 0] = f.x;
                 hx[4 * q + 1] = f.y;
                 hx[4 * q + 2] = f.z;
@@ -350,10 +408,15 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
         }
         Q4Act qh;
         q4_act_from_floats(hx, qh);
+#pragma unroll
+        for (int k = 0; k < NSD; ++k) sc_dn[k * WAVE + lane] = qd_s[k];
+        __builtin_amdgcn_wave_barrier();
+        const uint16_t* sd = reinterpret_cast<const uint16_t*>(sc_dn);
         float acc[DR];
 #pragma unroll
         for (int i = 0; i < DR; ++i) {
-            const float y = f16_bits_to_f32(dsv[i]) * q4_chunk_dot8(dv[i], qh);
+            const uint32_t si = (static_cast<uint32_t>(gi) * DR + i) * (d.I / LX_GROUP) + (dc * 32) / LX_GROUP;
+            const float y = f16_bits_to_f32(sd[si]) * q4_chunk_dot8(dv[i], qh);
             acc[i] = act ? y : 0.f;
         }
         // lane l holds the total of row (l >> SH) & (DR - 1) of group l >> SEG
@@ -440,10 +503,15 @@ bool layer_cfg(const MoeDims& d, LayerCfg& c)
     }
     const uint32_t rw = (64u >> c.seg) * c.dr;
     if (d.D % rw) return false;
+    // down scales of a wave's rows: 16-byte pieces, at most NSD per lane
+    if ((rw * d.I / 32) % 16 || rw * d.I / 512 > 64u * ((rw * (c.seg == 5 ? 1024u : 2048u) / 512 + 63) / 64))
+        return false;
     c.n_down = d.D / rw;
     // 6 gate/up rows per wave where that gives every wave a row block: less
     // dot-product work per wave than 8 rows on 3/4 of them
-    c.rb = (d.I % 6 == 0 && d.I / 6 == c.n_down) ? 6 : LX_UP_RB;
+    c.rb = (d.I % 6 == 0 && d.I / 6 == c.n_down && (6 * d.D / 32) % 16 == 0) ? 6 : LX_UP_RB;
+    // gate/up scales of a wave's rows: 16-byte pieces, one per lane
+    if ((c.rb * d.D / 32) % 16 || c.rb * d.D / 512 > 64) return false;
     c.n_up = d.I / c.rb;
     c.nbx = std::max(c.n_up, c.n_down);
     // every wave produces a router row or a gate/up row block
@@ -486,14 +554,20 @@ hipError_t dispatch(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_
 
 }  // namespace
 
-bool layer_supported(const MoeDims& d)
+bool layer_supported(const MoeDims& d, const LayerDesc& L)
 {
-    return dispatch(d, LayerDesc{}, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, true) == hipSuccess;
+    // 16-byte pieces of every tensor (the reference's blobs place tensors
+    // back to back with sizes that are multiples of 16)
+    bool aligned = reinterpret_cast<uintptr_t>(L.experts) % 16 == 0 && L.stride % 16 == 0;
+    for (int i = 0; i < 6; ++i) aligned = aligned && L.off[i] % 16 == 0;
+    return aligned &&
+           dispatch(d, LayerDesc{}, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, true) == hipSuccess;
 }
 
 hipError_t launch_moe_layer(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx, uint32_t* ids,
                             float* w, uint32_t* err, hipStream_t s)
 {
+    if (!layer_supported(d, L)) return hipErrorInvalidValue;
     return dispatch(d, L, hidden, lx, ids, w, err, s, false);
 }
 

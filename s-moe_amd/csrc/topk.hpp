@@ -322,24 +322,45 @@ __device__ __forceinline__ uint32_t top8_positions(const float (&v)[2], uint32_t
     return min(pos, n - 1);
 }
 
+// topk_net in two steps, so that a caller can act on the proposed ranks
+// while the softmax and the check run: topk_net_begin builds the keys and
+// runs the network; topk_net_rank(s, r) is the position the network proposes
+// for rank r (uniform r < 8; what topk_net_finish returns for rank r whenever
+// the check passes); topk_net_finish completes as topk_net.
+struct NetTopk {
+    uint32_t key[2];
+    uint32_t c[8];
+    bool bad;
+};
+
+__device__ __forceinline__ void topk_net_begin(const float (&v)[2], uint32_t n, NetTopk& s)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    // keys; a non-finite score fails the final check (the network's result is
+    // then unused)
+    s.bad = false;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t pos = lane + WAVE * j;
+        s.bad |= pos < n && !isfinite(v[j]);
+        s.key[j] = pos < n ? ((order_bits(v[j]) & ~127u) | (127u - pos)) : 0u;
+    }
+    net_top8(s.key[0], s.key[1], s.c);
+}
+
+__device__ __forceinline__ uint32_t topk_net_rank(const NetTopk& s, uint32_t r, uint32_t n)
+{
+    return min(127u - (sorted_at(s.c, r) & 127u), n - 1);
+}
+
 template <int VPL>
-__device__ uint32_t topk_net(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t norm, uint32_t& my_id, float& my_w,
-                             uint2* slots)
+__device__ uint32_t topk_net_finish(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t norm, uint32_t& my_id,
+                                    float& my_w, uint2* slots, const NetTopk& s)
 {
     static_assert(VPL == 2, "topk_net holds two positions per lane");
     const int lane = threadIdx.x & (WAVE - 1);
     const uint32_t count = k < n ? k : n;
     if (count != 0 && count <= 8 && n <= 128) {
-        // keys; a non-finite score fails the final check (the network's
-        // result is then unused)
-        uint32_t key[2];
-        bool bad = false;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t pos = lane + WAVE * j;
-            bad |= pos < n && !isfinite(v[j]);
-            key[j] = pos < n ? ((order_bits(v[j]) & ~127u) | (127u - pos)) : 0u;
-        }
         // softmax, as topk_fast
         float m = -INFINITY;
 #pragma unroll
@@ -355,25 +376,22 @@ __device__ uint32_t topk_net(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t n
         sum = wave_sum(sum);
         const float inv_sum = (sum > 0.f) ? 1.0f / sum : 0.f;
 
-        uint32_t c[8];
-        net_top8(key[0], key[1], c);
-
         // probabilities: of every position, of the proposed ranks (lane r),
         // and the largest over the unselected positions
-        const uint32_t last = sorted_at(c, count - 1);
+        const uint32_t last = sorted_at(s.c, count - 1);
         float p[2], rest = -1.f;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             p[j] = e[j] * inv_sum;
-            if (lane + WAVE * j < n && key[j] < last) rest = fmaxf(rest, p[j]);
+            if (lane + WAVE * j < n && s.key[j] < last) rest = fmaxf(rest, p[j]);
         }
         rest = wave_max(rest);
-        const uint32_t pos = 127u - (sorted_at(c, static_cast<uint32_t>(lane) & 7u) & 127u);
+        const uint32_t pos = 127u - (sorted_at(s.c, static_cast<uint32_t>(lane) & 7u) & 127u);
         const float q0 = __shfl(p[0], static_cast<int>(pos & 63u));
         const float q1 = __shfl(p[1], static_cast<int>(pos & 63u));
         const float pr = static_cast<uint32_t>(lane) < count ? (pos >= 64u ? q1 : q0) : rest;
         const float next = dpp_f32<DPP_ROW_SHL1>(-1.f, pr);   // lane r + 1's
-        if (__ballot(bad || (static_cast<uint32_t>(lane) < count && !(pr > next))) == 0) {
+        if (__ballot(s.bad || (static_cast<uint32_t>(lane) < count && !(pr > next))) == 0) {
             float ksum = 0.f;
 #pragma unroll
             for (int r = 0; r < 8; ++r)   // rank order, as the reference (x + 0 = x)
@@ -385,6 +403,15 @@ __device__ uint32_t topk_net(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t n
         }
     }
     return topk_fast<VPL>(v, n, k, norm, my_id, my_w, slots);
+}
+
+template <int VPL>
+__device__ uint32_t topk_net(float (&v)[VPL], uint32_t n, uint32_t k, uint32_t norm, uint32_t& my_id, float& my_w,
+                             uint2* slots)
+{
+    NetTopk s;
+    topk_net_begin(v, n, s);
+    return topk_net_finish<VPL>(v, n, k, norm, my_id, my_w, slots, s);
 }
 
 // The latency-bound callers (one row per wave on the critical path): the
