@@ -39,7 +39,7 @@ CONFIGS = {
 HBM_PEAK_GBS = 8000.0
 SEED = 20261201
 KERNEL_SYMBOLS = {"moe_up": "k_moe_up", "moe_down": "k_down_combine", "decode_stack": "k_decode_stack",
-                  "moe_layer": "k_moe_layer", "decode_spec": "k_decode_spec"}
+                  "moe_layer": "k_moe_layer", "decode_spec": "k_decode_spec", "moe_chain": "k_moe_chain"}
 
 
 def log(msg):
@@ -56,6 +56,7 @@ def kernel_bytes(c):
     return {
         "decode_stack": c["layers"] * (K * 3 * mat + 2 * E * D + 12 * D),
         "decode_spec": c["layers"] * (K * 3 * mat + 2 * E * D + 12 * D),
+        "moe_chain": c["layers"] * (K * 3 * mat + 2 * E * D + 12 * D),
         # the whole block: router bf16 + norm weights + 8 experts' gate/up/down + hidden in and out
         "moe_layer": K * 3 * mat + 2 * E * D + 2 * D + 8 * D,
         # router bf16 + norm weights + hidden in + 8 experts' gate+up + h out
@@ -95,7 +96,7 @@ def main():
     ap.add_argument("--replicas", type=int, default=4, help="prefill/batched: layer replicas rotated")
     ap.add_argument("--layers", type=int, default=0, help="override the layer count (0: config's)")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a graph")
-    ap.add_argument("--engine", default="stack", choices=("stack", "split", "persistent", "prefetch", "layers"),
+    ap.add_argument("--engine", default="chain", choices=("stack", "split", "persistent", "prefetch", "chain", "layers"),
                     help="stack: smoe_hip_moe_decode_stack, per-layer launches (one per layer where the shape "
                          "allows); split: the same with two launches per layer; persistent: the whole step in "
                          "one persistent launch; prefetch: the whole step in one persistent launch that "
@@ -182,8 +183,9 @@ def main():
     layer_arr = (smoe_amd.SmoeMoeLayer * NL)(*layers)
 
     ctx.set_decode_engine({"persistent": smoe_amd.DECODE_PERSISTENT, "prefetch": smoe_amd.DECODE_PREFETCH,
+                           "chain": smoe_amd.DECODE_CHAIN,
                            "split": smoe_amd.DECODE_SPLIT}.get(args.engine, smoe_amd.DECODE_LAUNCHES))
-    if args.engine in ("stack", "split", "persistent", "prefetch"):
+    if args.engine in ("stack", "split", "persistent", "prefetch", "chain"):
 
         def step():
             ctx.moe_decode_stack(shape, layer_arr, hidden.data_ptr())
@@ -242,6 +244,8 @@ def main():
                               "persistent": "stack API, one persistent launch per step",
                               "prefetch": "stack API, one persistent launch per step, next layer's predicted "
                                           "experts prefetched to LDS",
+                              "chain": "stack API, one launch per step running the one-launch layer schedule "
+                                       "layer after layer",
                               "layers": "one decode call per layer"}[args.engine],
                    "resident_expert_bytes": NL * E * raw},
     }
@@ -325,7 +329,7 @@ def _read_profile(ctx, smoe_amd):
     out = {}
     for kid, name in ((smoe_amd.KERNEL_MOE_UP, "moe_up"), (smoe_amd.KERNEL_MOE_DOWN, "moe_down"),
                       (smoe_amd.KERNEL_STACK, "decode_stack"), (smoe_amd.KERNEL_MOE_LAYER, "moe_layer"),
-                      (smoe_amd.KERNEL_STACK_PREFETCH, "decode_spec")):
+                      (smoe_amd.KERNEL_STACK_PREFETCH, "decode_spec"), (smoe_amd.KERNEL_CHAIN, "moe_chain")):
         n, ms = ctx.profile_read(kid)
         if n:
             out[name] = (n, ms * 1e3 / n)

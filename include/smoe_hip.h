@@ -246,9 +246,9 @@ int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
  *   for l in 0 .. n_layers-1:  hidden += MoE_l(RMSNorm_l(hidden))
  * with layers [n_layers] a host array of layer descriptors (all of one shape).
  * ids_out / weights_out [n_layers x top_k] are optional device outputs (rank
- * order, renormalised, decode.cpp:285-307).  Two engines
+ * order, renormalised, decode.cpp:285-307).  Engines
  * (smoe_hip_set_decode_engine):
- *   SMOE_DECODE_LAUNCHES (default): exactly n_layers smoe_hip_moe_decode
+ *   SMOE_DECODE_LAUNCHES: exactly n_layers smoe_hip_moe_decode
  *     calls (one or two launches per layer, as that entry point chooses).
  *   SMOE_DECODE_SPLIT: the same calls, always two launches per layer.
  *   SMOE_DECODE_PERSISTENT: the whole step in one persistent kernel launch
@@ -266,7 +266,15 @@ int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
  *     up to 768 (Qwen3-30B-A3B), on a device with 256 CUs; others take the
  *     launches.  Table handling as SMOE_DECODE_PERSISTENT.  Opt-in: at the
  *     30B shape it is currently slower per layer than SMOE_DECODE_LAUNCHES
- *     (copies in flight on a CU lengthen its exchange waits). */
+ *     (copies in flight on a CU lengthen its exchange waits).
+ *   SMOE_DECODE_CHAIN (default): the whole step in one launch that runs, layer after
+ *     layer, the single-launch layer kernel's schedule (one top-k rank per
+ *     XCD); every XCD combines all rows into its own copy of the next
+ *     layer's input, so layer l + 1 starts inside the launch as soon as its
+ *     XCD's copy is complete, with its router rows already requested.
+ *     Shapes: those of the single-launch layer kernel whose registers allow
+ *     a whole grid at once (Qwen3-30B-A3B); others take the launches.  Table
+ *     handling as SMOE_DECODE_PERSISTENT. */
 int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
                               const SmoeMoeLayer* layers, uint32_t n_layers, float* hidden,
                               uint32_t* ids_out, float* weights_out);
@@ -275,6 +283,7 @@ int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
 #define SMOE_DECODE_PERSISTENT 1
 #define SMOE_DECODE_SPLIT      2
 #define SMOE_DECODE_PREFETCH   3
+#define SMOE_DECODE_CHAIN      4
 /* Select the engine of smoe_hip_moe_decode_stack (and, for SMOE_DECODE_SPLIT,
  * the form of smoe_hip_moe_decode) for this context. */
 int smoe_hip_set_decode_engine(SmoeMetalCtx* ctx, int engine);
@@ -460,6 +469,7 @@ int smoe_hip_moe_decode_static(const SmoeMoeShape* shape, const SmoeMoeLayer* la
 #define SMOE_KERNEL_ATTENTION    14   /* dense trunk: QK norm/RoPE/KV append + decode attention   */
 #define SMOE_KERNEL_STREAM       15   /* measurement: streaming-read ceiling (smoe_hip_stream_read) */
 #define SMOE_KERNEL_STACK_PREFETCH 16 /* decode: every layer in one launch, predicted experts prefetched to LDS */
+#define SMOE_KERNEL_CHAIN        17 /* decode: every layer in one launch, the one-launch layer's schedule per layer */
 #define SMOE_KERNEL_KINDS        20
 int smoe_hip_profile_enable(SmoeMetalCtx* ctx, int enable);
 int smoe_hip_profile_read(SmoeMetalCtx* ctx, uint32_t kernel, uint64_t* launches, double* total_ms);

@@ -70,6 +70,19 @@ struct StackScratch {
     std::vector<LayerDesc> host_tbl;   // what tbl holds
 };
 
+// the chained decode kernel: exchange words, per-XCD hidden copies and
+// counters (zeroed once; the kernel keeps them), routing outputs nobody asked for
+struct ChainScratch {
+    size_t words = 0;               // capacity of xch
+    uint64_t* xch = nullptr;
+    size_t hcopy_n = 0;             // capacity of hcopy (floats)
+    float* hcopy = nullptr;
+    uint32_t* cnt = nullptr;        // [chain_cnt_words()]
+    size_t out_n = 0;               // capacity of ids / w
+    uint32_t* ids = nullptr;
+    float* w = nullptr;
+};
+
 }  // namespace
 
 struct SmoeMetalCtx {
@@ -95,7 +108,8 @@ struct SmoeMetalCtx {
     DeviceScratch ds;
     PrefillScratch ps;
     StackScratch ss;
-    int decode_engine = SMOE_DECODE_LAUNCHES;   // smoe_hip_moe_decode_stack's engine
+    ChainScratch cs;
+    int decode_engine = SMOE_DECODE_CHAIN;      // smoe_hip_moe_decode_stack's engine
     uint32_t* d_err = nullptr;       // [1] device-side error flags (bit 0: exchange time-out, bit 1: bad expert id)
     uint32_t* perm_pairs = nullptr;  // smoe_hip_permute's sorted pair ids
     float* mv_in = nullptr;          // reference-surface GEMV staging
@@ -406,6 +420,11 @@ extern "C" void smoe_metal_destroy(SmoeMetalCtx* ctx)
     dfree(ctx->ss.xch);
     dfree(ctx->ss.ctl);
     dfree(ctx->ss.tbl);
+    dfree(ctx->cs.xch);
+    dfree(ctx->cs.hcopy);
+    dfree(ctx->cs.cnt);
+    dfree(ctx->cs.ids);
+    dfree(ctx->cs.w);
     dfree(ctx->perm_pairs);
     dfree(ctx->mv_in);
     dfree(ctx->mv_out);
@@ -733,7 +752,7 @@ extern "C" int smoe_hip_stream_read(SmoeMetalCtx* ctx, const void* src, uint64_t
 extern "C" int smoe_hip_set_decode_engine(SmoeMetalCtx* ctx, int engine)
 {
     if (!ctx || (engine != SMOE_DECODE_LAUNCHES && engine != SMOE_DECODE_PERSISTENT && engine != SMOE_DECODE_SPLIT &&
-                 engine != SMOE_DECODE_PREFETCH))
+                 engine != SMOE_DECODE_PREFETCH && engine != SMOE_DECODE_CHAIN))
         return SMOE_ERR_ARG;
     ctx->decode_engine = engine;
     return SMOE_OK;
@@ -791,6 +810,80 @@ static bool same_layer(const LayerDesc& a, const LayerDesc& b)
     return std::memcmp(&a, &b, sizeof(LayerDesc)) == 0;
 }
 
+// the device copy of the layer table, uploaded when it changes (outside
+// capture: under capture a new table gives SMOE_ERR_CAPTURE)
+static int upload_table(SmoeMetalCtx* ctx, const SmoeMoeLayer* layers, uint32_t n_layers)
+{
+    StackScratch& s = ctx->ss;
+    bool same = s.tbl && s.host_tbl.size() == n_layers;
+    for (uint32_t l = 0; same && l < n_layers; ++l) same = same_layer(s.host_tbl[l], layer_of(&layers[l]));
+    if (same) return SMOE_OK;
+    if (stream_capturing(ctx->stream)) return SMOE_ERR_CAPTURE;
+    std::vector<LayerDesc> t(n_layers);
+    for (uint32_t l = 0; l < n_layers; ++l) t[l] = layer_of(&layers[l]);
+    // the previous table may still be read by queued work
+    if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
+    if (s.tbl_cap < n_layers) {
+        dfree(s.tbl);
+        s.tbl_cap = 0;
+        if (!dalloc(ctx, &s.tbl, n_layers)) return SMOE_ERR_HIP;
+        s.tbl_cap = n_layers;
+    }
+    if (!hip_ok(ctx, hipMemcpy(s.tbl, t.data(), n_layers * sizeof(LayerDesc), hipMemcpyHostToDevice),
+                "hipMemcpy(layer table)"))
+        return SMOE_ERR_HIP;
+    s.host_tbl = std::move(t);
+    return SMOE_OK;
+}
+
+// SMOE_DECODE_CHAIN: the whole step in one launch of k_moe_chain
+static int decode_chain(SmoeMetalCtx* ctx, const MoeDims& d, const SmoeMoeLayer* layers, uint32_t n_layers,
+                        float* hidden, uint32_t* ids_out, float* weights_out)
+{
+    ChainScratch& c = ctx->cs;
+    const size_t words = smoe::chain_xch_words(d.D, d.E, d.I);
+    const size_t hn = size_t(8) * d.D, outn = size_t(n_layers) * d.K;
+    if (c.words < words || c.hcopy_n < hn || !c.cnt || (!ids_out && c.out_n < outn) || (!weights_out && c.out_n < outn)) {
+        if (stream_capturing(ctx->stream)) return SMOE_ERR_CAPTURE;
+        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
+        if (c.words < words) {
+            dfree(c.xch);
+            c.words = 0;
+            if (!dalloc(ctx, &c.xch, words) ||
+                !hip_ok(ctx, hipMemset(c.xch, 0, words * sizeof(uint64_t)), "hipMemset(chain xch)"))
+                return SMOE_ERR_HIP;
+            c.words = words;
+        }
+        if (c.hcopy_n < hn) {
+            dfree(c.hcopy);
+            c.hcopy_n = 0;
+            if (!dalloc(ctx, &c.hcopy, hn)) return SMOE_ERR_HIP;
+            c.hcopy_n = hn;
+        }
+        if (!c.cnt && (!dalloc(ctx, &c.cnt, smoe::chain_cnt_words()) ||
+                       !hip_ok(ctx, hipMemset(c.cnt, 0, smoe::chain_cnt_words() * sizeof(uint32_t)),
+                               "hipMemset(chain counters)")))
+            return SMOE_ERR_HIP;
+        if (c.out_n < outn) {
+            dfree(c.ids);
+            dfree(c.w);
+            c.out_n = 0;
+            if (!dalloc(ctx, &c.ids, outn) || !dalloc(ctx, &c.w, outn)) return SMOE_ERR_HIP;
+            c.out_n = outn;
+        }
+    }
+    const int rc = upload_table(ctx, layers, n_layers);
+    if (rc != SMOE_OK) return rc;
+    if (!timed(ctx, SMOE_KERNEL_CHAIN, "moe_chain", [&] {
+            return smoe::launch_moe_chain(d, ctx->ss.tbl, n_layers, hidden, c.xch, c.hcopy, c.cnt,
+                                          ids_out ? ids_out : c.ids, weights_out ? weights_out : c.w, ctx->d_err,
+                                          ctx->stream);
+        }))
+        return SMOE_ERR_HIP;
+    ctx->dispatches.fetch_add(uint64_t(n_layers) * d.K, std::memory_order_relaxed);
+    return SMOE_OK;
+}
+
 extern "C" int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, const SmoeMoeLayer* layers,
                                          uint32_t n_layers, float* hidden, uint32_t* ids_out, float* weights_out)
 {
@@ -800,6 +893,12 @@ extern "C" int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* 
     int rc = shape_check(shape);
     if (rc != SMOE_OK) return rc;
     const MoeDims d = dims_of(shape);
+    if (ctx->decode_engine == SMOE_DECODE_CHAIN) {
+        std::vector<LayerDesc> host(n_layers);
+        for (uint32_t l = 0; l < n_layers; ++l) host[l] = layer_of(&layers[l]);
+        if (smoe::chain_supported(d, host.data(), n_layers))
+            return decode_chain(ctx, d, layers, n_layers, hidden, ids_out, weights_out);
+    }
     const bool spec = ctx->decode_engine == SMOE_DECODE_PREFETCH && smoe::spec_supported(d);
     if (!spec && (ctx->decode_engine != SMOE_DECODE_PERSISTENT || !smoe::stack_supported(d))) {
         // two launches per layer
@@ -833,25 +932,8 @@ extern "C" int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* 
         s.words = words;
     }
     // device layer table: uploaded when it changes (outside capture)
-    bool same = s.tbl && s.host_tbl.size() == n_layers;
-    for (uint32_t l = 0; same && l < n_layers; ++l) same = same_layer(s.host_tbl[l], layer_of(&layers[l]));
-    if (!same) {
-        if (capturing) return SMOE_ERR_CAPTURE;
-        std::vector<LayerDesc> t(n_layers);
-        for (uint32_t l = 0; l < n_layers; ++l) t[l] = layer_of(&layers[l]);
-        // the previous table may still be read by queued work
-        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
-        if (s.tbl_cap < n_layers) {
-            dfree(s.tbl);
-            s.tbl_cap = 0;
-            if (!dalloc(ctx, &s.tbl, n_layers)) return SMOE_ERR_HIP;
-            s.tbl_cap = n_layers;
-        }
-        if (!hip_ok(ctx, hipMemcpy(s.tbl, t.data(), n_layers * sizeof(LayerDesc), hipMemcpyHostToDevice),
-                    "hipMemcpy(layer table)"))
-            return SMOE_ERR_HIP;
-        s.host_tbl = std::move(t);
-    }
+    rc = upload_table(ctx, layers, n_layers);
+    if (rc != SMOE_OK) return rc;
     // one launch per ST_MAX_LAYERS layers (the kernel keeps its layer table in LDS)
     for (uint32_t l0 = 0; l0 < n_layers; l0 += smoe::ST_MAX_LAYERS) {
         const uint32_t n = std::min<uint32_t>(smoe::ST_MAX_LAYERS, n_layers - l0);

@@ -106,6 +106,22 @@ bool layer_supported(const MoeDims& d, const LayerDesc& L);
 // ids/w [K] receive the routing; err bit 0 reports an exchange time-out
 hipError_t launch_moe_layer(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx, uint32_t* ids,
                             float* w, uint32_t* err, hipStream_t s);
+// Every layer of a decode step in one launch with k_moe_layer's schedule per
+// layer.  xch: chain_xch_words(D, E, I) exchange words; hcopy [8 x D] floats;
+// cnt chain_cnt_words() words (per-XCD row-block flags, then an abort word);
+// all zero at allocation and never re-armed
+// (calls on one set must not overlap).  layers_dev: the layer table in device
+// memory; ids/w [n_layers x K].
+constexpr uint32_t CHAIN_FLAGS = 256;       // row-block flags per XCD (n_down <= 256)
+__host__ __device__ constexpr size_t chain_xch_words(uint32_t D, uint32_t E, uint32_t I)
+{
+    return lx_words(D, E, I) + 8ull * lx_pad(D);
+}
+constexpr size_t chain_cnt_words() { return 8 * CHAIN_FLAGS + 64; }
+bool chain_supported(const MoeDims& d, const LayerDesc* layers_host, uint32_t n_layers);
+hipError_t launch_moe_chain(const MoeDims& d, const LayerDesc* layers_dev, uint32_t n_layers, float* hidden,
+                            uint64_t* xch, float* hcopy, uint32_t* cnt, uint32_t* ids, float* w, uint32_t* err,
+                            hipStream_t s);
 // out[slot * out_stride + row] = down_slot . h_slot   (per-expert outputs)
 hipError_t launch_down_slots(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n_exp,
                              const float* h, uint32_t h_stride, float* out,

@@ -74,14 +74,52 @@ __device__ __forceinline__ uint64_t get_agent(const uint64_t* p)
 {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ uint32_t get_agent32(const uint32_t* p)
+{
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// drop this CU's L1 lines (data other CUs of the XCD rewrote in the L2
+// since they were read is then read from the L2)
+__device__ __forceinline__ void l1_invalidate()
+{
+    asm volatile("buffer_inv sc0" ::: "memory");
+}
+__device__ __forceinline__ void vm_wait_all()
+{
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// Where one layer step reads its input and leaves its output.
+struct LayerIO {
+    const float* hin;        // the layer's input hidden state [D]
+    const uint32_t* wait;    // null, or: the input is complete once wait[0 .. n_down - 1]
+    uint32_t wait_tag;       // all equal wait_tag; it was written by other CUs of this XCD
+                             // during the launch (read from the L2, not from a stale L1)
+    float* hout;             // combined rows go here (null: none)
+    bool all_rows;           // every wave combines its row block for its own XCD
+                             // (else: row block t on XCD t % 8, once)
+    uint32_t* flag;          // null, or: flag[t] = tag once the wave's combined rows are stored
+    uint64_t* py;            // the rank partials' exchange words
+    uint32_t* abort;         // null, or: a wave that times out stores abort_val here, and
+    uint32_t abort_val;      // every wait ends once it reads abort_val
+};
+
+// a bounded wait's spin count: true once the wait is to end unfinished
+__device__ __forceinline__ bool give_up(uint32_t spins, const LayerIO& io)
+{
+    if (spins > LX_SPIN_LIMIT) return true;
+    return io.abort && (spins & 255u) == 0 && get_agent32(io.abort) == io.abort_val;
+}
 
 }  // namespace
 
+// One layer of one token, by wave t of XCD x (nbx waves per XCD).  Returns
+// true when one of its waits timed out.
 template <int CPL, int VPL, int SEG, int DR, int RB>
-__global__ __launch_bounds__(WAVE)
-void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* __restrict__ lx,
-                 uint32_t* __restrict__ ids_out, float* __restrict__ w_out, uint32_t n_up, uint32_t n_down,
-                 uint32_t* __restrict__ err)
+__device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc& L, const LayerIO& io,
+                                               uint64_t* __restrict__ lx, uint32_t tag, uint32_t* ids_out,
+                                               float* w_out, uint32_t n_up, uint32_t n_down, uint32_t t, uint32_t x,
+                                               uint32_t nbx)
 {
     constexpr int NR = RB == 6 ? 16 : 2 * RB;   // reduced values (gate, up per row), padded to a power of two
     constexpr int GL = 1 << SEG;       // lanes of one down group
@@ -90,20 +128,14 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
     constexpr int SH = SEG - ilog2(DR);
     const int lane = threadIdx.x & (WAVE - 1);
     const uint32_t D = d.D, nch = D >> 5;
-    const uint32_t nbx = gridDim.x >> 3;
-    const uint32_t t = blockIdx.x >> 3;
-    const uint32_t x = xcc_id();
-
-    uint32_t tag = static_cast<uint32_t>(get_agent(lx)) + 1u;
-    tag = __builtin_amdgcn_readfirstlane(tag ? tag : 1u);
     uint64_t* logc = lx + LX_HEAD + x * lx_pad(d.E);
     uint64_t* hxc = lx + LX_HEAD + 8u * lx_pad(d.E) + x * lx_pad(d.I);
-    uint64_t* py = lx + LX_HEAD + 8u * lx_pad(d.E) + 8u * lx_pad(d.I);
+    uint64_t* py = io.py;
     const uint32_t py_stride = lx_pad(D);
     bool timed_out = false;
 
-
-    // 1. hidden, norm weight and router rows t, t + nbx
+    // 1. norm weights and router rows t, t + nbx (they do not depend on the
+    //    hidden state: requested before waiting for it), then the hidden state
     const bool producer = t < d.E;
     const bool second = t + nbx < d.E;
     float4 xv[CPL][8];
@@ -111,8 +143,6 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const uint32_t c = min(lane + WAVE * j, nch - 1);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) xv[j][q] = load_f4(hidden + c * 32 + q * 4);
 #pragma unroll
         for (int q = 0; q < 4; ++q) g[j][q] = load_u4(L.norm_w + c * 32 + q * 8);
     }
@@ -133,6 +163,30 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
                 for (int q = 0; q < 4; ++q) rw2[j][q] = load_u4(wr2 + c * 32 + q * 8);
             }
         }
+    }
+    if (io.wait) {
+        // the row blocks' flags, as the logit exchange polls its words
+        uint32_t spins = 0;
+        bool all;
+        do {
+            all = true;
+            for (uint32_t k = lane; k < n_down; k += WAVE) all &= get_agent32(io.wait + k) == io.wait_tag;
+            all = __ballot(!all) == 0;
+            if (!all) {
+                if (give_up(++spins, io)) {
+                    timed_out = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        } while (!all);
+        l1_invalidate();
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xv[j][q] = load_f4(io.hin + c * 32 + q * 4);
     }
     // 2. RMS norm: normed = (x * inv) * w, inv = 1 / sqrt(ss / n + 1e-6)
     float ss = 0.f;
@@ -218,7 +272,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
                 all &= pos >= d.E || static_cast<uint32_t>(w64 >> 32) == tag;
             }
             all = __ballot(!all) == 0;
-            if (!all && ++spins > LX_SPIN_LIMIT) {
+            if (!all && give_up(++spins, io)) {
                 timed_out = true;
                 break;
             }
@@ -385,7 +439,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
                 }
                 all = __ballot(!all) == 0;
                 if (!all) {
-                    if (++spins > LX_SPIN_LIMIT) {
+                    if (give_up(++spins, io)) {
                         timed_out = true;
                         break;
                     }
@@ -425,8 +479,9 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
         const uint32_t myrow = t * RW + (lane >> SEG) * DR + ((lane >> SH) & (DR - 1));
         if (holder) put_agent(py + x * py_stride + myrow, lx_word(tot, tag));
 
-        // 5. combine of row block t on XCD t % 8, in rank order
-        if ((t & 7u) == x) {
+        // 5. combine of row block t (on XCD t % 8, or on every XCD for its own
+        //    copy), in rank order
+        if ((io.all_rows ? true : (t & 7u) == x) && io.hout) {
             const int src = ((lane / DR) << SEG) | ((lane % DR) << SH);   // holder of row t*RW + lane
             const float own = __shfl(tot, src & (WAVE - 1));
             if (lane < RW) {
@@ -444,7 +499,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
                         y[r] = mine ? own : __uint_as_float(static_cast<uint32_t>(w64));
                         all &= mine || static_cast<uint32_t>(w64 >> 32) == tag;
                     }
-                    if (!all && ++spins > LX_SPIN_LIMIT) {
+                    if (!all && give_up(++spins, io)) {
                         timed_out = true;
                         break;
                     }
@@ -452,15 +507,99 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
                 float sum = 0.f;
 #pragma unroll
                 for (int r = 0; r < 8; ++r) sum = fmaf(readlane_f32(my_w, r), y[r], sum);
-                hidden[row] = hidden[row] + sum;
+                // (the input as this wave read it at the start of the layer: no
+                // other wave writes these rows before this one)
+                io.hout[row] = io.hin[row] + sum;
             }
-            if (x == 0 && t == 0) {
-                __builtin_amdgcn_wave_barrier();
-                if (lane == 0) put_agent(lx, static_cast<uint64_t>(tag));
+            if (io.flag) {
+                // the rows are in the L2 before the flag says so
+                vm_wait_all();
+                if (lane == 0) __hip_atomic_store(io.flag + t, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
             }
         }
     }
-    if (timed_out) atomicOr(err, 1u);
+    if (timed_out && io.abort && lane == 0)
+        __hip_atomic_store(io.abort, io.abort_val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return timed_out;
+}
+
+template <int CPL, int VPL, int SEG, int DR, int RB>
+__global__ __launch_bounds__(WAVE)
+void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* __restrict__ lx,
+                 uint32_t* __restrict__ ids_out, float* __restrict__ w_out, uint32_t n_up, uint32_t n_down,
+                 uint32_t* __restrict__ err)
+{
+    const uint32_t nbx = gridDim.x >> 3;
+    const uint32_t t = blockIdx.x >> 3;
+    const uint32_t x = xcc_id();
+    uint32_t tag = static_cast<uint32_t>(get_agent(lx)) + 1u;
+    tag = __builtin_amdgcn_readfirstlane(tag ? tag : 1u);
+    LayerIO io{};
+    io.hin = hidden;
+    io.hout = hidden;
+    io.py = lx + LX_HEAD + 8u * lx_pad(d.E) + 8u * lx_pad(d.I);
+    const bool to = moe_layer_step<CPL, VPL, SEG, DR, RB>(d, L, io, lx, tag, ids_out, w_out, n_up, n_down, t, x, nbx);
+    // the combiner of row block 0 on XCD 0 advances the epoch
+    if (x == 0 && t == 0 && t < n_down) {
+        __builtin_amdgcn_wave_barrier();
+        if ((threadIdx.x & (WAVE - 1)) == 0) put_agent(lx, static_cast<uint64_t>(tag));
+    }
+    if (to) atomicOr(err, 1u);
+}
+
+// Every layer of a decode step in one launch: the wave schedule of
+// k_moe_layer per layer, with each XCD combining every row into its own copy
+// of the next layer's input (in its L2; one flag per row block, carrying the
+// layer's tag, says when it is complete) and the last layer combining into
+// `hidden` on XCD 0.  The flags and the copy are only ever read by the XCD
+// that wrote them, after the flags, past the CU's L1.  Tags: epoch + l + 1 for layer l; the rank partials
+// alternate between two sets of words by layer parity (an XCD can start
+// layer l + 1's partials while another XCD still reads layer l's, never layer
+// l - 1's: that needs every XCD's layer l partials).  A wave that times out
+// stores the abort word, after which every wait of the launch ends.
+template <int CPL, int VPL, int SEG, int DR, int RB>
+__global__ __launch_bounds__(WAVE)
+void k_moe_chain(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_layers, float* __restrict__ hidden,
+                 uint64_t* __restrict__ lx, float* __restrict__ hcopy, uint32_t* __restrict__ cnt,
+                 uint32_t* __restrict__ ids_out, float* __restrict__ w_out, uint32_t n_up, uint32_t n_down,
+                 uint32_t* __restrict__ err)
+{
+    const uint32_t nbx = gridDim.x >> 3;
+    const uint32_t t = blockIdx.x >> 3;
+    const uint32_t x = xcc_id();
+    // read by every wave before any of them can change them (a change needs
+    // every wave's router rows of layer 0)
+    const uint32_t ep0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(get_agent(lx)));
+    uint32_t* flags_x = cnt + x * CHAIN_FLAGS;
+    float* hx = hcopy + static_cast<size_t>(x) * d.D;
+    uint64_t* py0 = lx + LX_HEAD + 8u * lx_pad(d.E) + 8u * lx_pad(d.I);
+    bool to = false;
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        const LayerDesc L = layers[l];
+        const bool last = l + 1 == n_layers;
+        LayerIO io{};
+        uint32_t tag = ep0 + l + 1u, prev = ep0 + l;
+        tag = tag ? tag : 1u;
+        prev = prev ? prev : 1u;
+        io.hin = l == 0 ? hidden : hx;
+        io.wait = l > 0 ? flags_x : nullptr;
+        io.wait_tag = prev;
+        io.hout = last ? (x == 0 ? hidden : nullptr) : hx;
+        io.all_rows = true;
+        io.flag = last ? nullptr : flags_x;
+        io.py = py0 + (l & 1u) * 8u * lx_pad(d.D);
+        io.abort = cnt + 8 * CHAIN_FLAGS;
+        io.abort_val = ep0 + 1u;
+        to |= moe_layer_step<CPL, VPL, SEG, DR, RB>(d, L, io, lx, tag, ids_out + l * d.K, w_out + l * d.K, n_up,
+                                                     n_down, t, x, nbx);
+    }
+    // wave 0 of XCD 0 advances the epoch once its last combine is done (that
+    // needs every wave's last partials)
+    if (x == 0 && t == 0) {
+        __builtin_amdgcn_wave_barrier();
+        if ((threadIdx.x & (WAVE - 1)) == 0) put_agent(lx, static_cast<uint64_t>(ep0 + n_layers));
+    }
+    if (to) atomicOr(err, 1u);
 }
 
 namespace {
@@ -470,16 +609,19 @@ struct LayerCfg {
     uint32_t n_up, n_down, nbx;
 };
 
-template <int CPL, int VPL, int SEG, int DR, int RB>
+template <int CPL, int VPL, int SEG, int DR, int RB, bool CHAIN>
 uint32_t resident_blocks()
 {
     static uint32_t cap = [] {
         int dev = 0, per_cu = 0, cus = 0;
         if (hipGetDevice(&dev) != hipSuccess) return 0u;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0u;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_layer<CPL, VPL, SEG, DR, RB>, WAVE, 0) !=
-            hipSuccess)
-            return 0u;
+        hipError_t e;
+        if constexpr (CHAIN)
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_chain<CPL, VPL, SEG, DR, RB>, WAVE, 0);
+        else
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_layer<CPL, VPL, SEG, DR, RB>, WAVE, 0);
+        if (e != hipSuccess) return 0u;
         return static_cast<uint32_t>(per_cu) * static_cast<uint32_t>(cus);
     }();
     return cap;
@@ -519,27 +661,46 @@ bool layer_cfg(const MoeDims& d, LayerCfg& c)
     return true;
 }
 
+// the arguments of a launch of either kernel (chain: `layers` [n_layers],
+// hcopy and cnt set)
+struct LaunchArgs {
+    const LayerDesc* L = nullptr;       // one layer (host struct)
+    const LayerDesc* layers = nullptr;  // the chain's table (device)
+    uint32_t n_layers = 0;
+    float* hidden = nullptr;
+    uint64_t* lx = nullptr;
+    float* hcopy = nullptr;
+    uint32_t* cnt = nullptr;
+    uint32_t* ids = nullptr;
+    float* w = nullptr;
+    uint32_t* err = nullptr;
+};
+
 template <int CPL, int VPL, int SEG, int DR, int RB>
-hipError_t launch_cfg(const LayerCfg& c, const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx,
-                      uint32_t* ids, float* w, uint32_t* err, hipStream_t s, bool dry)
+hipError_t launch_cfg(const LayerCfg& c, const MoeDims& d, const LaunchArgs& a, bool chain, hipStream_t s, bool dry)
 {
-    if (8u * c.nbx > resident_blocks<CPL, VPL, SEG, DR, RB>()) return hipErrorInvalidConfiguration;
+    const uint32_t cap = chain ? resident_blocks<CPL, VPL, SEG, DR, RB, true>()
+                               : resident_blocks<CPL, VPL, SEG, DR, RB, false>();
+    if (8u * c.nbx > cap || (chain && c.n_down > CHAIN_FLAGS)) return hipErrorInvalidConfiguration;
     if (dry) return hipSuccess;
-    launch_kernel(k_moe_layer<CPL, VPL, SEG, DR, RB>, dim3(8u * c.nbx), dim3(WAVE), s, d, L, hidden, lx, ids, w, c.n_up,
-                  c.n_down, err);
+    if (chain)
+        launch_kernel(k_moe_chain<CPL, VPL, SEG, DR, RB>, dim3(8u * c.nbx), dim3(WAVE), s, d, a.layers, a.n_layers,
+                      a.hidden, a.lx, a.hcopy, a.cnt, a.ids, a.w, c.n_up, c.n_down, a.err);
+    else
+        launch_kernel(k_moe_layer<CPL, VPL, SEG, DR, RB>, dim3(8u * c.nbx), dim3(WAVE), s, d, *a.L, a.hidden, a.lx,
+                      a.ids, a.w, c.n_up, c.n_down, a.err);
     return hipGetLastError();
 }
 
-hipError_t dispatch(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx, uint32_t* ids, float* w,
-                    uint32_t* err, hipStream_t s, bool dry)
+hipError_t dispatch(const MoeDims& d, const LaunchArgs& a, bool chain, hipStream_t s, bool dry)
 {
     LayerCfg c;
     if (!layer_cfg(d, c)) return hipErrorInvalidValue;
 #define SMOE_LAYER_CASE(C, V, S, R)                                                           \
     if (c.cpl == C && c.vpl == V && c.seg == S && c.dr == R && c.rb == 8)                     \
-        return launch_cfg<C, V, S, R, 8>(c, d, L, hidden, lx, ids, w, err, s, dry);           \
+        return launch_cfg<C, V, S, R, 8>(c, d, a, chain, s, dry);                             \
     if (c.cpl == C && c.vpl == V && c.seg == S && c.dr == R && c.rb == 6)                     \
-        return launch_cfg<C, V, S, R, 6>(c, d, L, hidden, lx, ids, w, err, s, dry);
+        return launch_cfg<C, V, S, R, 6>(c, d, a, chain, s, dry);
     SMOE_LAYER_CASE(1, 2, 5, 8)
     SMOE_LAYER_CASE(1, 2, 6, 32)
     SMOE_LAYER_CASE(1, 8, 5, 8)
@@ -554,21 +715,56 @@ hipError_t dispatch(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_
 
 }  // namespace
 
-bool layer_supported(const MoeDims& d, const LayerDesc& L)
+static bool layer_aligned(const LayerDesc& L)
 {
     // 16-byte pieces of every tensor (the reference's blobs place tensors
     // back to back with sizes that are multiples of 16)
     bool aligned = reinterpret_cast<uintptr_t>(L.experts) % 16 == 0 && L.stride % 16 == 0;
     for (int i = 0; i < 6; ++i) aligned = aligned && L.off[i] % 16 == 0;
-    return aligned &&
-           dispatch(d, LayerDesc{}, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, true) == hipSuccess;
+    return aligned;
+}
+
+bool layer_supported(const MoeDims& d, const LayerDesc& L)
+{
+    return layer_aligned(L) && dispatch(d, LaunchArgs{}, false, nullptr, true) == hipSuccess;
 }
 
 hipError_t launch_moe_layer(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx, uint32_t* ids,
                             float* w, uint32_t* err, hipStream_t s)
 {
     if (!layer_supported(d, L)) return hipErrorInvalidValue;
-    return dispatch(d, L, hidden, lx, ids, w, err, s, false);
+    LaunchArgs a;
+    a.L = &L;
+    a.hidden = hidden;
+    a.lx = lx;
+    a.ids = ids;
+    a.w = w;
+    a.err = err;
+    return dispatch(d, a, false, s, false);
+}
+
+bool chain_supported(const MoeDims& d, const LayerDesc* layers_host, uint32_t n_layers)
+{
+    for (uint32_t l = 0; l < n_layers; ++l)
+        if (!layer_aligned(layers_host[l])) return false;
+    return n_layers > 0 && dispatch(d, LaunchArgs{}, true, nullptr, true) == hipSuccess;
+}
+
+hipError_t launch_moe_chain(const MoeDims& d, const LayerDesc* layers_dev, uint32_t n_layers, float* hidden,
+                            uint64_t* xch, float* hcopy, uint32_t* cnt, uint32_t* ids, float* w, uint32_t* err,
+                            hipStream_t s)
+{
+    LaunchArgs a;
+    a.layers = layers_dev;
+    a.n_layers = n_layers;
+    a.hidden = hidden;
+    a.lx = xch;
+    a.hcopy = hcopy;
+    a.cnt = cnt;
+    a.ids = ids;
+    a.w = w;
+    a.err = err;
+    return dispatch(d, a, true, s, false);
 }
 
 }  // namespace smoe

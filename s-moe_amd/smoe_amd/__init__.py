@@ -136,12 +136,12 @@ SIGNATURES = [
 KERNEL_MOE_UP, KERNEL_GATE_UP, KERNEL_MOE_DOWN, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
 KERNEL_PERMUTE, KERNEL_GROUPED_GATE_UP, KERNEL_GROUPED_DOWN, KERNEL_SCATTER = 5, 6, 7, 8
 KERNEL_ROUTE, KERNEL_SPLIT, KERNEL_STACK, KERNEL_MOE_LAYER = 9, 10, 11, 12
-KERNEL_GEMV, KERNEL_ATTENTION, KERNEL_STREAM, KERNEL_STACK_PREFETCH = 13, 14, 15, 16
-DECODE_LAUNCHES, DECODE_PERSISTENT, DECODE_SPLIT, DECODE_PREFETCH = 0, 1, 2, 3
+KERNEL_GEMV, KERNEL_ATTENTION, KERNEL_STREAM, KERNEL_STACK_PREFETCH, KERNEL_CHAIN = 13, 14, 15, 16, 17
+DECODE_LAUNCHES, DECODE_PERSISTENT, DECODE_SPLIT, DECODE_PREFETCH, DECODE_CHAIN = 0, 1, 2, 3, 4
 KERNEL_NAMES = {0: "moe_up", 1: "gate_up", 2: "moe_down", 3: "down_slots", 4: "topk",
                 5: "permute", 6: "grouped_gate_up", 7: "grouped_down", 8: "combine", 9: "route",
                 10: "split", 11: "decode_stack", 12: "moe_layer", 13: "gemv", 14: "attention",
-                15: "stream_read", 16: "decode_spec"}
+                15: "stream_read", 16: "decode_spec", 17: "moe_chain"}
 
 _lib = None
 

@@ -15,14 +15,14 @@ from gpu_helpers import Layer, hidden_states, moe_delta_err, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
-ENGINES = [smoe_amd.DECODE_PERSISTENT, smoe_amd.DECODE_LAUNCHES]
+ENGINES = [smoe_amd.DECODE_PERSISTENT, smoe_amd.DECODE_LAUNCHES, smoe_amd.DECODE_CHAIN]
 
 
-@pytest.fixture(params=ENGINES, ids=["persistent", "launches"])
+@pytest.fixture(params=ENGINES, ids=["persistent", "launches", "chain"])
 def engine(ctx, request):
     ctx.set_decode_engine(request.param)
     yield request.param
-    ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
+    ctx.set_decode_engine(smoe_amd.DECODE_CHAIN)
 
 
 def run_stack(ctx, layers, hid):
@@ -126,7 +126,7 @@ def test_stack_matches_per_layer_decode(ctx, engine):
         ctx.moe_decode(l.shape, l.layer, b.data_ptr(), 1, ids[i].data_ptr())
     ctx.synchronize()
     assert (ids.cpu().numpy().view(np.uint32) == fids).all()
-    if engine == smoe_amd.DECODE_LAUNCHES:
+    if engine in (smoe_amd.DECODE_LAUNCHES, smoe_amd.DECODE_CHAIN):
         assert torch.equal(a, b)
     x = x0.cpu().numpy().astype(np.float64)
     da, db = a.cpu().numpy() - x, b.cpu().numpy() - x
