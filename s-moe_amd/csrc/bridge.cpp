@@ -407,6 +407,8 @@ extern "C" SmoeMetalCtx* smoe_metal_init(size_t slot_bytes)
     // the allocation-free decode entry point's per-device scratch (its address
     // and first clearing), here so that later calls need no set-up
     (void)smoe::static_scratch_setup();
+    // how the device deals blocks over its XCDs (the one-launch decode kernels need round-robin)
+    (void)smoe::deal_probe();
     return ctx;
 }
 

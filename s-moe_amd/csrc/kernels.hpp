@@ -99,8 +99,13 @@ __host__ __device__ constexpr size_t lx_words(uint32_t D, uint32_t E, uint32_t I
 {
     return LX_HEAD + 8ull * (lx_pad(E) + lx_pad(I) + lx_pad(D));
 }
-// true when k == 8, the shape's grid fits on the device at once and the
-// layer's tensors are 16-byte aligned
+// Checks once per device (synchronously, outside stream capture) that blocks
+// are dealt round-robin over the 8 XCDs, which the one-launch layer kernels
+// rely on; later calls return the cached answer.
+bool deal_probe();
+// true when k == 8, the shape's grid fits on the device at once, the layer's
+// tensors are 16-byte aligned and the device deals blocks round-robin (as
+// deal_probe found; false before it ran)
 bool layer_supported(const MoeDims& d, const LayerDesc& L);
 // the whole MoE block of one token: hidden [D] += MoE(RMSNorm(hidden));
 // ids/w [K] receive the routing; err bit 0 reports an exchange time-out

@@ -36,6 +36,9 @@
 // err bit 0.  The whole grid must be resident at once: the host checks it
 // against the occupancy of the kernel.
 #include <algorithm>
+#include <cstdio>
+#include <mutex>
+#include <vector>
 
 #include "device_common.hpp"
 #include "kernels.hpp"
@@ -715,6 +718,62 @@ hipError_t dispatch(const MoeDims& d, const LaunchArgs& a, bool chain, hipStream
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// The layer kernels take a wave's XCD-local index from its block id (t = b / 8
+// on XCD XCC_ID), which holds when the dispatcher deals consecutive blocks
+// round-robin over the 8 XCDs.  Checked once per device (at context set-up):
+// a grid of one-wave blocks records each block's XCC_ID; anything but
+// (XCC_ID - b) mod 8 constant over the grid turns both kernels off (their
+// shapes then take the two-launch path, which does not depend on it).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(WAVE) void k_deal_probe(uint32_t* out)
+{
+    if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
+namespace {
+constexpr uint32_t DEAL_BLOCKS = 4096;   // >= 8 x the most waves per XCD a layer kernel launches
+constexpr int DEAL_MAX_DEVICES = 64;
+std::mutex g_deal_mu;
+int g_deal[DEAL_MAX_DEVICES] = {};       // 0 unknown, 1 round-robin, 2 not
+}  // namespace
+
+bool deal_probe()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= DEAL_MAX_DEVICES) return false;
+    std::lock_guard<std::mutex> lock(g_deal_mu);
+    if (g_deal[dev]) return g_deal[dev] == 1;
+    hipStream_t s = nullptr;
+    uint32_t* buf = nullptr;
+    std::vector<uint32_t> h(DEAL_BLOCKS, 8u);
+    bool ran = hipStreamCreateWithFlags(&s, hipStreamNonBlocking) == hipSuccess &&
+               hipMalloc(&buf, DEAL_BLOCKS * sizeof(uint32_t)) == hipSuccess;
+    if (ran) {
+        hipLaunchKernelGGL(k_deal_probe, dim3(DEAL_BLOCKS), dim3(WAVE), 0, s, buf);
+        ran = hipGetLastError() == hipSuccess && hipStreamSynchronize(s) == hipSuccess &&
+              hipMemcpy(h.data(), buf, DEAL_BLOCKS * sizeof(uint32_t), hipMemcpyDeviceToHost) == hipSuccess;
+    }
+    if (buf) (void)hipFree(buf);
+    if (s) (void)hipStreamDestroy(s);
+    if (!ran) return false;   // unknown: tried again at the next set-up
+    bool rr = h[0] < 8;
+    for (uint32_t b = 1; rr && b < DEAL_BLOCKS; ++b) rr = h[b] == ((h[0] + b) & 7u);
+    if (!rr)
+        std::fprintf(stderr, "[smoe_hip] blocks are not dealt round-robin over 8 XCDs on device %d: the one-launch "
+                             "decode kernels are off, decode takes two launches per layer\n", dev);
+    g_deal[dev] = rr ? 1 : 2;
+    return rr;
+}
+
+static bool deal_known_round_robin()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= DEAL_MAX_DEVICES) return false;
+    std::lock_guard<std::mutex> lock(g_deal_mu);
+    return g_deal[dev] == 1;
+}
+
 static bool layer_aligned(const LayerDesc& L)
 {
     // 16-byte pieces of every tensor (the reference's blobs place tensors
@@ -726,7 +785,7 @@ static bool layer_aligned(const LayerDesc& L)
 
 bool layer_supported(const MoeDims& d, const LayerDesc& L)
 {
-    return layer_aligned(L) && dispatch(d, LaunchArgs{}, false, nullptr, true) == hipSuccess;
+    return layer_aligned(L) && deal_known_round_robin() && dispatch(d, LaunchArgs{}, false, nullptr, true) == hipSuccess;
 }
 
 hipError_t launch_moe_layer(const MoeDims& d, const LayerDesc& L, float* hidden, uint64_t* lx, uint32_t* ids,
@@ -747,7 +806,7 @@ bool chain_supported(const MoeDims& d, const LayerDesc* layers_host, uint32_t n_
 {
     for (uint32_t l = 0; l < n_layers; ++l)
         if (!layer_aligned(layers_host[l])) return false;
-    return n_layers > 0 && dispatch(d, LaunchArgs{}, true, nullptr, true) == hipSuccess;
+    return n_layers > 0 && deal_known_round_robin() && dispatch(d, LaunchArgs{}, true, nullptr, true) == hipSuccess;
 }
 
 hipError_t launch_moe_chain(const MoeDims& d, const LayerDesc* layers_dev, uint32_t n_layers, float* hidden,
