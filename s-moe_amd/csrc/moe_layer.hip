@@ -137,12 +137,24 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     const uint32_t py_stride = lx_pad(D);
     bool timed_out = false;
 
-    // 1. norm weights and router rows t, t + nbx (they do not depend on the
-    //    hidden state: requested before waiting for it), then the hidden state
+    // 1. the hidden state, norm weights and router rows t, t + nbx.  Loads
+    //    return in order, so the hidden state goes first (the norm can then
+    //    start while the router rows arrive) -- unless the input is still to
+    //    be waited for: then the norm weights and router rows are requested
+    //    first, and the hidden state once it is complete.
     const bool producer = t < d.E;
     const bool second = t + nbx < d.E;
     float4 xv[CPL][8];
     uint4 g[CPL][4], rw[CPL][4], rw2[CPL][4];
+    auto load_hidden = [&] {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) xv[j][q] = load_f4(io.hin + c * 32 + q * 4);
+        }
+    };
+    if (!io.wait) load_hidden();
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const uint32_t c = min(lane + WAVE * j, nch - 1);
@@ -184,12 +196,7 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
             }
         } while (!all);
         l1_invalidate();
-    }
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        const uint32_t c = min(lane + WAVE * j, nch - 1);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) xv[j][q] = load_f4(io.hin + c * 32 + q * 4);
+        load_hidden();
     }
     // 2. RMS norm: normed = (x * inv) * w, inv = 1 / sqrt(ss / n + 1e-6)
     float ss = 0.f;
@@ -308,25 +315,34 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     const bool act = static_cast<uint32_t>(c0) < CH;
     const uint32_t dc = act ? static_cast<uint32_t>(c0) : CH - 1;
     const uint32_t rowb = t * RW + gi * DR;
-    // The scales of the wave's rows are contiguous (RB * D / 32 bytes of
-    // gate, as many of up, RW * I / 32 of down): one 16-byte piece per lane
-    // (a load instruction costs the CU a request slot whatever its width),
-    // issued ahead of the rows and passed to the lanes that use them through
-    // LDS.  Host-checked: the pieces are 16-byte aligned and the gate/up
-    // ones fit one per lane.
+    // GATHER (the configurations with PROPOSE): the scales of the wave's rows
+    // are contiguous (RB * D / 32 bytes of gate, as many of up, RW * I / 32
+    // of down), loaded as one 16-byte piece per lane (a load instruction
+    // costs the CU a request slot whatever its width: at 30B this halves the
+    // gate/up requests the top-k check waits behind), issued ahead of the rows
+    // and passed to the lanes that use them through LDS.  Host-checked: the
+    // pieces are 16-byte aligned and the gate/up ones fit one per lane.  The
+    // wide configurations load each lane's scale beside its row piece (the
+    // LDS hand-over costs the 235B layer 2.8 us).
+    constexpr bool GATHER = PROPOSE;
     constexpr uint32_t DN_MAX_I = SEG == 5 ? 1024u : 2048u;
-    constexpr int NSD = (RW * DN_MAX_I / 512 + WAVE - 1) / WAVE;   // down scale pieces per lane
+    constexpr int NSD = GATHER ? (RW * DN_MAX_I / 512 + WAVE - 1) / WAVE : 1;   // down scale pieces per lane
     const uint32_t nsq_up = RB * D / 512, nsq_dn = RW * d.I / 512;
     uint4 va[RB][CPL], vb[RB][CPL], qa_s, qb_s, qd_s[NSD];
+    uint16_t sva[GATHER ? 1 : RB][CPL], svb[GATHER ? 1 : RB][CPL], dsv[GATHER ? 1 : DR];
     uint4 dv[DR];
-    __shared__ uint4 sc_up[2][WAVE];
+    __shared__ uint4 sc_up[GATHER ? 2 : 1][WAVE];
     __shared__ uint4 sc_dn[NSD * WAVE];
     auto issue_up = [&](const uint8_t* blob) {
         const uint8_t* pa = blob + L.off[0];
         const uint8_t* pb = blob + L.off[2];
-        const uint32_t q = min(static_cast<uint32_t>(lane), nsq_up - 1);
-        qa_s = load_stream_u4(blob + L.off[1] + static_cast<size_t>(rowg) * row_scales * 2 + q * 16);
-        qb_s = load_stream_u4(blob + L.off[3] + static_cast<size_t>(rowg) * row_scales * 2 + q * 16);
+        const uint16_t* sa = reinterpret_cast<const uint16_t*>(blob + L.off[1]);
+        const uint16_t* sb = reinterpret_cast<const uint16_t*>(blob + L.off[3]);
+        if constexpr (GATHER) {
+            const uint32_t q = min(static_cast<uint32_t>(lane), nsq_up - 1);
+            qa_s = load_stream_u4(blob + L.off[1] + static_cast<size_t>(rowg) * row_scales * 2 + q * 16);
+            qb_s = load_stream_u4(blob + L.off[3] + static_cast<size_t>(rowg) * row_scales * 2 + q * 16);
+        }
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
             const size_t row = rowg + i;
@@ -335,21 +351,29 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
                 const uint32_t c = min(lane + WAVE * j, nch - 1);
                 va[i][j] = load_stream_u4(pa + row * row_bytes + c * 16);
                 vb[i][j] = load_stream_u4(pb + row * row_bytes + c * 16);
+                if constexpr (!GATHER) {
+                    sva[i][j] = load_stream_u16(sa + row * row_scales + (c * 32) / LX_GROUP);
+                    svb[i][j] = load_stream_u16(sb + row * row_scales + (c * 32) / LX_GROUP);
+                }
             }
         }
     };
     auto issue_down = [&](const uint8_t* blob) {
         const uint8_t* pdn = blob + L.off[4];
-        const uint32_t drow_bytes = d.I >> 1;
+        const uint16_t* sdn = reinterpret_cast<const uint16_t*>(blob + L.off[5]);
+        const uint32_t drow_bytes = d.I >> 1, drow_scales = d.I / LX_GROUP;
+        if constexpr (GATHER) {
 #pragma unroll
-        for (int k = 0; k < NSD; ++k) {
-            const uint32_t q = min(static_cast<uint32_t>(k * WAVE + lane), nsq_dn - 1);
-            qd_s[k] = load_stream_u4(blob + L.off[5] + static_cast<size_t>(t) * RW * (d.I / 32) + q * 16);
+            for (int k = 0; k < NSD; ++k) {
+                const uint32_t q = min(static_cast<uint32_t>(k * WAVE + lane), nsq_dn - 1);
+                qd_s[k] = load_stream_u4(blob + L.off[5] + static_cast<size_t>(t) * RW * (d.I / 32) + q * 16);
+            }
         }
 #pragma unroll
         for (int i = 0; i < DR; ++i) {
             const size_t row = rowb + i;
             dv[i] = load_stream_u4(pdn + row * drow_bytes + dc * 16);
+            if constexpr (!GATHER) dsv[i] = load_stream_u16(sdn + row * drow_scales + (dc * 32) / LX_GROUP);
         }
     };
     const uint8_t* blob;
@@ -377,11 +401,13 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     if (t < n_up) {
         if constexpr (!PROPOSE) issue_up(blob);
         __builtin_amdgcn_sched_barrier(0);
-        sc_up[0][lane] = qa_s;
-        sc_up[1][lane] = qb_s;
-        __builtin_amdgcn_wave_barrier();
+        if constexpr (GATHER) {
+            sc_up[0][lane] = qa_s;
+            sc_up[GATHER ? 1 : 0][lane] = qb_s;
+            __builtin_amdgcn_wave_barrier();
+        }
         const uint16_t* sga = reinterpret_cast<const uint16_t*>(sc_up[0]);
-        const uint16_t* sgb = reinterpret_cast<const uint16_t*>(sc_up[1]);
+        const uint16_t* sgb = reinterpret_cast<const uint16_t*>(sc_up[GATHER ? 1 : 0]);
         float part[NR];
 #pragma unroll
         for (int i = 2 * RB; i < NR; ++i) part[i] = 0.f;
@@ -391,8 +417,10 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 const uint32_t si = i * row_scales + (min(lane + WAVE * j, nch - 1) * 32) / LX_GROUP;
-                ga = fmaf(f16_bits_to_f32(sga[si]), q4_chunk_dot8(va[i][j], qa[j]), ga);
-                ua = fmaf(f16_bits_to_f32(sgb[si]), q4_chunk_dot8(vb[i][j], qa[j]), ua);
+                const uint16_t s_a = GATHER ? sga[si] : sva[GATHER ? 0 : i][j];
+                const uint16_t s_b = GATHER ? sgb[si] : svb[GATHER ? 0 : i][j];
+                ga = fmaf(f16_bits_to_f32(s_a), q4_chunk_dot8(va[i][j], qa[j]), ga);
+                ua = fmaf(f16_bits_to_f32(s_b), q4_chunk_dot8(vb[i][j], qa[j]), ua);
             }
             part[2 * i] = ga;
             part[2 * i + 1] = ua;
@@ -415,13 +443,17 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
         issue_down(blob);
         // all of this XCD's h, staged in LDS: passes of 16 words per lane,
         // every load of a pass in flight before any is checked (addresses
-        // past the end re-read word I - 1).  Quad-major: quad q (values 4q ..
-        // 4q + 3) of 32-value chunk c at float4 q * (CH + 1) + c, so the 64
-        // lanes reading quad q of their chunks touch consecutive addresses
-        // (the + 1 spreads the writes of a pass over the banks).
+        // past the end re-read word I - 1).  GATHER configurations store it
+        // quad-major: quad q (values 4q .. 4q + 3) of 32-value chunk c at
+        // float4 q * (CH + 1) + c, so the 64 lanes reading quad q of their
+        // chunks touch consecutive addresses (the + 1 spreads the writes of a
+        // pass over the banks); the wide ones (two passes of writes per round)
+        // keep h in order, which measured 1.1 us faster at 235B.
         __shared__ __align__(16) float h_s[8 * (LX_MAX_I / 32 + 1) * 4];
         const uint32_t chp = CH + 1;
-        auto hpos = [&](uint32_t k) { return (((k & 31u) >> 2) * chp + (k >> 5)) * 4u + (k & 3u); };
+        auto hpos = [&](uint32_t k) {
+            return GATHER ? (((k & 31u) >> 2) * chp + (k >> 5)) * 4u + (k & 3u) : k;
+        };
         {
             const uint32_t passes = (d.I + 16 * WAVE - 1) / (16 * WAVE);
             uint32_t spins = 0;
@@ -456,7 +488,7 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
             const float4* hp = reinterpret_cast<const float4*>(h_s);
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                const float4 f = hp[q * chp + dc];
+                const float4 f = hp[GATHER ? q * chp + dc : dc * 8 + q];
                 hx[4 * q + 0] = f.x;
                 hx[4 * q + 1] = f.y;
                 hx[4 * q + 2] = f.z;
@@ -465,15 +497,17 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
         }
         Q4Act qh;
         q4_act_from_floats(hx, qh);
+        if constexpr (GATHER) {
 #pragma unroll
-        for (int k = 0; k < NSD; ++k) sc_dn[k * WAVE + lane] = qd_s[k];
-        __builtin_amdgcn_wave_barrier();
+            for (int k = 0; k < NSD; ++k) sc_dn[k * WAVE + lane] = qd_s[k];
+            __builtin_amdgcn_wave_barrier();
+        }
         const uint16_t* sd = reinterpret_cast<const uint16_t*>(sc_dn);
         float acc[DR];
 #pragma unroll
         for (int i = 0; i < DR; ++i) {
             const uint32_t si = (static_cast<uint32_t>(gi) * DR + i) * (d.I / LX_GROUP) + (dc * 32) / LX_GROUP;
-            const float y = f16_bits_to_f32(sd[si]) * q4_chunk_dot8(dv[i], qh);
+            const float y = f16_bits_to_f32(GATHER ? sd[si] : dsv[GATHER ? 0 : i]) * q4_chunk_dot8(dv[i], qh);
             acc[i] = act ? y : 0.f;
         }
         // lane l holds the total of row (l >> SH) & (DR - 1) of group l >> SEG
