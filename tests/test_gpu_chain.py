@@ -119,11 +119,25 @@ def test_chain_repeated_calls_shape_change_and_graph_replay(ctx, chain):
         assert torch.equal(junk, ref)
 
 
-def test_chain_other_shapes_take_the_launches(ctx, chain):
-    """A shape the chained kernel does not take (the 235B layer) runs as
-    per-layer launches under the chain engine, with the same results."""
-    layers = [Layer(ctx, 4096, 128, 8, 1536, layer_id=240 + i, host=False) for i in range(2)]
+def test_chain_235b_shape_equals_layer_calls(ctx, chain):
+    """At the 235B shape the chain engine equals the per-layer launches bit
+    for bit."""
+    layers = [Layer(ctx, 4096, 128, 8, 1536, layer_id=240 + i, host=False) for i in range(3)]
     x0 = hidden_states(ctx, 1, 4096, 34)[0]
+    a = x0.clone()
+    aids, aw = run_stack(ctx, layers, a)
+    ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
+    b = x0.clone()
+    bids, bw = run_stack(ctx, layers, b)
+    assert torch.equal(a, b) and (aids == bids).all() and (aw == bw).all()
+
+
+def test_chain_other_shapes_take_the_launches(ctx, chain):
+    """A shape the chained kernel does not take (d_model 4096: it would spill
+    registers) runs as per-layer launches under the chain engine, with the
+    same results."""
+    layers = [Layer(ctx, 4096, 128, 8, 1536, layer_id=250 + i, host=False) for i in range(2)]
+    x0 = hidden_states(ctx, 1, 4096, 35)[0]
     a = x0.clone()
     ctx.profile_enable(True)
     run_stack(ctx, layers, a)
