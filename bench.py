@@ -49,16 +49,17 @@ def log(msg):
 def kernel_bytes(c):
     """Algorithmic HBM bytes per launch of each decode kernel: one token-layer
     for the one- and two-launch paths; one token through every layer for the
-    stack kernel (per layer k * B_expert + 2 E D router + 12 D for x, hidden in
-    and hidden out)."""
+    whole-step kernels (per layer the same bytes as one k_moe_layer launch:
+    k * B_expert + 2 E D router + 2 D norm weights + 4 D hidden in + 4 D out)."""
     D, E, K, I = c["D"], c["E"], c["K"], c["I"]
     mat = D * I // 2 + D * I // 64 * 2            # packed nibbles + fp16 scales of one matrix
+    # the whole block: router bf16 + norm weights + 8 experts' gate/up/down + hidden in and out
+    layer = K * 3 * mat + 2 * E * D + 2 * D + 8 * D
     return {
-        "decode_stack": c["layers"] * (K * 3 * mat + 2 * E * D + 12 * D),
-        "decode_spec": c["layers"] * (K * 3 * mat + 2 * E * D + 12 * D),
-        "moe_chain": c["layers"] * (K * 3 * mat + 2 * E * D + 12 * D),
-        # the whole block: router bf16 + norm weights + 8 experts' gate/up/down + hidden in and out
-        "moe_layer": K * 3 * mat + 2 * E * D + 2 * D + 8 * D,
+        "decode_stack": c["layers"] * layer,
+        "decode_spec": c["layers"] * layer,
+        "moe_chain": c["layers"] * layer,
+        "moe_layer": layer,
         # router bf16 + norm weights + hidden in + 8 experts' gate+up + h out
         "moe_up": E * D * 2 + D * 2 + D * 4 + K * 2 * mat + K * I * 4,
         # 8 experts' down + h in + weights + hidden read and written

@@ -103,7 +103,7 @@ def test_layer_matches_split_form(ctx, D, E, K, I):
         b.copy_(x0)
         ib, wb = decode(ctx, layer, b)
     finally:
-        ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
+        ctx.set_decode_engine(smoe_amd.DECODE_CHAIN)
     assert (ia == ib).all() and np.array_equal(wa, wb)
     x = x0.cpu().numpy().astype(np.float64)
     da, db = a.cpu().numpy() - x, b.cpu().numpy() - x

@@ -24,7 +24,7 @@ TOL = 1e-3
 def prefetch(ctx):
     ctx.set_decode_engine(smoe_amd.DECODE_PREFETCH)
     yield
-    ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
+    ctx.set_decode_engine(smoe_amd.DECODE_CHAIN)
 
 
 def run_stack(ctx, layers, hid):
@@ -93,7 +93,7 @@ def test_prefetch_stack_equals_layer_calls(ctx, oracle, prefetch, E, I, n):
     assert worst <= TOL
 
 
-def test_prefetch_matches_per_layer_engine(ctx):
+def test_prefetch_matches_per_layer_engine(ctx, prefetch):
     """Against the per-layer launch engine on the same 6 layers: same ids,
     hidden states within the tolerance of each other."""
     layers = [Layer(ctx, 2048, 128, 8, 768, layer_id=90 + i, host=False) for i in range(6)]
