@@ -81,6 +81,23 @@ def pmc_traffic(kernel, workload):
     return int(ent["traffic_bytes"]) if "traffic_bytes" in ent else None
 
 
+def calibrate_copy(args, dev):
+    """For PMC runs: a plain streaming kernel of known size, b = -a over N MiB
+    of fp32 (reads N MiB and writes N MiB), against which FETCH_SIZE and
+    WRITE_SIZE are scaled."""
+    if not args.calibrate_copy_mib:
+        return
+    import torch
+    n = (args.calibrate_copy_mib << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(4):
+        torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    del a, b
+    log(f"counter calibration: 4 x neg over {args.calibrate_copy_mib} MiB")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -113,7 +130,7 @@ def main():
     args = ap.parse_args()
 
     if args.rocprof_summary:
-        rocprof_summary(args.rocprof_summary, args.config, args.pmc_out, args.calibrate_copy_mib)
+        rocprof_summary(args.rocprof_summary, args.config, args.pmc_out, args.calibrate_copy_mib, args.workload)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -148,17 +165,7 @@ def main():
     torch.cuda.set_stream(stream)
     ctx.set_stream(stream.cuda_stream)
 
-    if args.calibrate_copy_mib:
-        # a plain streaming kernel of known size: b = -a over N MiB of fp32
-        # reads N MiB and writes N MiB
-        n = (args.calibrate_copy_mib << 20) // 4
-        a = torch.ones(n, dtype=torch.float32, device=dev)
-        b = torch.empty_like(a)
-        for _ in range(4):
-            torch.neg(a, out=b)
-        torch.cuda.synchronize()
-        del a, b
-        log(f"counter calibration: 4 x neg over {args.calibrate_copy_mib} MiB")
+    calibrate_copy(args, dev)
 
     shape = smoe_amd.make_shape(D, E, K, I)
     off, raw, stride = smoe_amd.blob_layout(D, I)
@@ -701,6 +708,7 @@ def grouped_bench(args):
     g = GROUPED[args.workload]
     D, E, K, I, T, R = g["D"], g["E"], g["K"], g["I"], g["T"], args.replicas
     dev = torch.device("cuda", 0)
+    calibrate_copy(args, dev)
     ctx = smoe_amd.Context()
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
@@ -803,7 +811,7 @@ def grouped_bench(args):
 # ---------------------------------------------------------------------------
 # rocprofv3 summaries (the text committed under profiles/)
 # ---------------------------------------------------------------------------
-def rocprof_summary(d, config, pmc_out, copy_mib):
+def rocprof_summary(d, config, pmc_out, copy_mib, workload="decode"):
     """Print a per-kernel summary of a rocprofv3 output directory: kernel
     stats (--kernel-trace --stats) and, for --pmc runs, the average counter
     value per dispatch of each kernel.  With --pmc-out (and the size given by
@@ -831,7 +839,12 @@ def rocprof_summary(d, config, pmc_out, copy_mib):
     if not (pmc_out and copy_mib):
         return
     data = json.load(open(pmc_out)) if os.path.exists(pmc_out) else {}
-    ent = data.setdefault(CONFIGS[config]["workload"], {})
+    if workload in GROUPED:
+        ent = data.setdefault(GROUPED[workload]["workload"], {})
+        symbols = ("k_grouped_mm<true>", "k_grouped_mm<false>")
+    else:
+        ent = data.setdefault(CONFIGS[config]["workload"], {})
+        symbols = tuple(KERNEL_SYMBOLS.values())
     for cn in ("FETCH_SIZE", "WRITE_SIZE"):
         copies = [tot / n for (k, c2), (tot, n) in acc.items() if c2 == cn and "neg_kernel" in k]
         if not copies:
@@ -840,7 +853,7 @@ def rocprof_summary(d, config, pmc_out, copy_mib):
         scale = copy_mib * 1024.0 / copy_kib        # expected KiB / measured KiB for the copy
         data.setdefault("_calibration", {})[cn] = {"copy_mib": copy_mib, "copy_kib_measured": round(copy_kib, 1),
                                                     "scale": round(scale, 4)}
-        for sym in KERNEL_SYMBOLS.values():
+        for sym in symbols:
             vals = [tot / n for (k, c2), (tot, n) in acc.items() if c2 == cn and sym in k]
             if vals:
                 e = ent.setdefault(sym, {})
