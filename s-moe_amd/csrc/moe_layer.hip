@@ -724,10 +724,11 @@ struct LayerCfg {
 };
 
 // Waves per block where the block shares its loads: the wide (235B) family,
-// 6 waves, one block per CU (each wave would otherwise read 24 KB of hidden
-// state and norm weights: 28.3 against 29.7 us per layer).  At the 30B shape
-// sharing measured no gain, and one-wave blocks are kept.
-constexpr int shared_nw(int cpl, int seg) { return cpl == 2 && seg == 6 ? 6 : 1; }
+// one block per CU of all the CU's waves, 8 or 6 (each wave would otherwise
+// read 24 KB of hidden state and norm weights: 28.3 against 29.7 us per layer
+// with 6).  At the 30B shape sharing measured no gain, and one-wave blocks
+// are kept.
+constexpr bool shares_loads(int cpl, int seg) { return cpl == 2 && seg == 6; }
 
 template <int CPL, int VPL, int SEG, int DR, int RB, bool CHAIN, int NW>
 auto kernel_of()
@@ -783,8 +784,10 @@ bool layer_cfg(const MoeDims& d, LayerCfg& c)
         c.seg = 5;
         c.dr = 8;
     } else {
+        // 16 down rows per wave where 6 gate/up rows then give every wave a row
+        // block of each (two equal waves per SIMD), else 32
         c.seg = 6;
-        c.dr = 32;
+        c.dr = (d.I % 6 == 0 && d.D % 16 == 0 && d.I / 6 == d.D / 16) ? 16 : 32;
     }
     const uint32_t rw = (64u >> c.seg) * c.dr;
     if (d.D % rw) return false;
@@ -839,12 +842,15 @@ hipError_t launch_nw(const LayerCfg& c, const MoeDims& d, const LaunchArgs& a, h
 template <int CPL, int VPL, int SEG, int DR, int RB>
 hipError_t launch_cfg(const LayerCfg& c, const MoeDims& d, const LaunchArgs& a, bool chain, hipStream_t s, bool dry)
 {
-    constexpr int NWS = shared_nw(CPL, SEG);
-    if constexpr (NWS > 1) {
-        // a block of shared loads where the grid divides into them
-        if (c.nbx % NWS == 0)
-            return chain ? launch_nw<CPL, VPL, SEG, DR, RB, true, NWS>(c, d, a, s, dry)
-                         : launch_nw<CPL, VPL, SEG, DR, RB, false, NWS>(c, d, a, s, dry);
+    if constexpr (shares_loads(CPL, SEG)) {
+        // a block of shared loads where the grid divides into them (one per CU:
+        // 256 or 192 waves an XCD)
+        if (c.nbx % 8 == 0)
+            return chain ? launch_nw<CPL, VPL, SEG, DR, RB, true, 8>(c, d, a, s, dry)
+                         : launch_nw<CPL, VPL, SEG, DR, RB, false, 8>(c, d, a, s, dry);
+        if (c.nbx % 6 == 0)
+            return chain ? launch_nw<CPL, VPL, SEG, DR, RB, true, 6>(c, d, a, s, dry)
+                         : launch_nw<CPL, VPL, SEG, DR, RB, false, 6>(c, d, a, s, dry);
     }
     return chain ? launch_nw<CPL, VPL, SEG, DR, RB, true, 1>(c, d, a, s, dry)
                  : launch_nw<CPL, VPL, SEG, DR, RB, false, 1>(c, d, a, s, dry);
@@ -860,12 +866,16 @@ hipError_t dispatch(const MoeDims& d, const LaunchArgs& a, bool chain, hipStream
     if (c.cpl == C && c.vpl == V && c.seg == S && c.dr == R && c.rb == 6)                     \
         return launch_cfg<C, V, S, R, 6>(c, d, a, chain, s, dry);
     SMOE_LAYER_CASE(1, 2, 5, 8)
+    SMOE_LAYER_CASE(1, 2, 6, 16)
     SMOE_LAYER_CASE(1, 2, 6, 32)
     SMOE_LAYER_CASE(1, 8, 5, 8)
+    SMOE_LAYER_CASE(1, 8, 6, 16)
     SMOE_LAYER_CASE(1, 8, 6, 32)
     SMOE_LAYER_CASE(2, 2, 5, 8)
+    SMOE_LAYER_CASE(2, 2, 6, 16)
     SMOE_LAYER_CASE(2, 2, 6, 32)
     SMOE_LAYER_CASE(2, 8, 5, 8)
+    SMOE_LAYER_CASE(2, 8, 6, 16)
     SMOE_LAYER_CASE(2, 8, 6, 32)
 #undef SMOE_LAYER_CASE
     return hipErrorInvalidValue;
