@@ -969,10 +969,11 @@ hipError_t launch_moe_layer(const MoeDims& d, const LayerDesc& L, float* hidden,
 
 bool chain_supported(const MoeDims& d, const LayerDesc* layers_host, uint32_t n_layers)
 {
-    // the narrow configurations (one chunk of 32 columns per lane): the wide
-    // ones would spill registers in the chained kernel (32.2 against 28.3 us
-    // per 235B layer for the per-layer launches)
-    if (d.D > 64 * 32) return false;
+    // the narrow configurations (one chunk of 32 columns per lane), and the
+    // wide ones with 16 down rows a wave: with 32 the chained kernel spilled
+    // registers (32.2 against 28.3 us per 235B layer for the per-layer launches)
+    LayerCfg c;
+    if (!layer_cfg(d, c) || (c.cpl != 1 && c.dr != 16)) return false;
     for (uint32_t l = 0; l < n_layers; ++l)
         if (!layer_aligned(layers_host[l])) return false;
     return n_layers > 0 && deal_known_round_robin() && dispatch(d, LaunchArgs{}, true, nullptr, true) == hipSuccess;

@@ -120,12 +120,16 @@ def test_chain_repeated_calls_shape_change_and_graph_replay(ctx, chain):
 
 
 def test_chain_235b_shape_equals_layer_calls(ctx, chain):
-    """At the 235B shape the chain engine equals the per-layer launches bit
-    for bit."""
+    """At the 235B shape the chain engine runs one chained launch and equals
+    the per-layer launches bit for bit."""
     layers = [Layer(ctx, 4096, 128, 8, 1536, layer_id=240 + i, host=False) for i in range(3)]
     x0 = hidden_states(ctx, 1, 4096, 34)[0]
     a = x0.clone()
+    ctx.profile_enable(True)
     aids, aw = run_stack(ctx, layers, a)
+    n, _ = ctx.profile_read(smoe_amd.KERNEL_CHAIN)
+    ctx.profile_enable(False)
+    assert n == 1
     ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
     b = x0.clone()
     bids, bw = run_stack(ctx, layers, b)
@@ -133,17 +137,18 @@ def test_chain_235b_shape_equals_layer_calls(ctx, chain):
 
 
 def test_chain_other_shapes_take_the_launches(ctx, chain):
-    """A shape the chained kernel does not take (d_model 4096: it would spill
-    registers) runs as per-layer launches under the chain engine, with the
-    same results."""
-    layers = [Layer(ctx, 4096, 128, 8, 1536, layer_id=250 + i, host=False) for i in range(2)]
+    """A shape the chained kernel does not take (d_model 4096 with 32 down
+    rows a wave: it would spill registers) runs as one-launch layer kernels
+    under the chain engine, with the same results as the launches engine."""
+    layers = [Layer(ctx, 4096, 128, 8, 1280, layer_id=250 + i, host=False) for i in range(2)]
     x0 = hidden_states(ctx, 1, 4096, 35)[0]
     a = x0.clone()
     ctx.profile_enable(True)
     run_stack(ctx, layers, a)
     n, _ = ctx.profile_read(smoe_amd.KERNEL_CHAIN)
+    m, _ = ctx.profile_read(smoe_amd.KERNEL_MOE_LAYER)
     ctx.profile_enable(False)
-    assert n == 0
+    assert (n, m) == (0, 2)
     ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
     b = x0.clone()
     run_stack(ctx, layers, b)
