@@ -121,7 +121,7 @@ __device__ __forceinline__ bool give_up(uint32_t spins, const LayerIO& io)
 // one copy of the hidden state and norm weights and one of the XCD's h in
 // LDS (the CU then reads them from the L2 once instead of once per wave); the
 // whole block calls the step.
-template <int CPL, int VPL, int SEG, int DR, int RB, int NW>
+template <int CPL, int VPL, int SEG, int DR, int RB, int NW, bool CHAIN>
 __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc& L, const LayerIO& io,
                                                uint64_t* __restrict__ lx, uint32_t tag, uint32_t* ids_out,
                                                float* w_out, uint32_t n_up, uint32_t n_down, uint32_t t, uint32_t x,
@@ -330,9 +330,11 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     uint2* slots = slots_all[wv];
     // Where the gate/up rows in flight leave registers for the rest of the
     // top-k: the expert of rank x as the top-k network proposes it (E <= 128),
-    // so its weights are requested while the softmax and the check run.
-    // Otherwise (more experts, or wide rows) the exact top-k first.
-    constexpr bool PROPOSE = VPL == 2 && RB * CPL * 2 * 4 <= 64;
+    // so its weights are requested while the softmax and the check run: the
+    // narrow configurations, and the wide ones with 6 rows a wave (two waves
+    // a SIMD) outside the chain (whose layer loop leaves too few registers).
+    // Otherwise (more experts, or 8 wide rows) the exact top-k first.
+    constexpr bool PROPOSE = VPL == 2 && (RB * CPL * 2 * 4 <= 64 || (CPL == 2 && RB == 6 && !CHAIN));
     uint32_t prop, expert;
     NetTopk net;
     if constexpr (PROPOSE) {
@@ -352,7 +354,7 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     const bool act = static_cast<uint32_t>(c0) < CH;
     const uint32_t dc = act ? static_cast<uint32_t>(c0) : CH - 1;
     const uint32_t rowb = t * RW + gi * DR;
-    // GATHER (the configurations with PROPOSE): the scales of the wave's rows
+    // GATHER (the narrow configurations with PROPOSE): the scales of the wave's rows
     // are contiguous (RB * D / 32 bytes of gate, as many of up, RW * I / 32
     // of down), loaded as one 16-byte piece per lane (a load instruction
     // costs the CU a request slot whatever its width: at 30B this halves the
@@ -361,7 +363,7 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     // pieces are 16-byte aligned and the gate/up ones fit one per lane.  The
     // wide configurations load each lane's scale beside its row piece (the
     // LDS hand-over costs the 235B layer 2.8 us).
-    constexpr bool GATHER = PROPOSE;
+    constexpr bool GATHER = PROPOSE && CPL == 1;
     constexpr uint32_t DN_MAX_I = SEG == 5 ? 1024u : 2048u;
     constexpr int NSD = GATHER ? (RW * DN_MAX_I / 512 + WAVE - 1) / WAVE : 1;   // down scale pieces per lane
     const uint32_t nsq_up = RB * D / 512, nsq_dn = RW * d.I / 512;
@@ -652,7 +654,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
     io.hout = hidden;
     io.py = lx + LX_HEAD + 8u * lx_pad(d.E) + 8u * lx_pad(d.I);
     const bool to =
-        moe_layer_step<CPL, VPL, SEG, DR, RB, NW>(d, L, io, lx, tag, ids_out, w_out, n_up, n_down, t, x, nbx);
+        moe_layer_step<CPL, VPL, SEG, DR, RB, NW, false>(d, L, io, lx, tag, ids_out, w_out, n_up, n_down, t, x, nbx);
     // the combiner of row block 0 on XCD 0 advances the epoch
     if (x == 0 && t == 0 && t < n_down) {
         __builtin_amdgcn_wave_barrier();
@@ -704,8 +706,8 @@ void k_moe_chain(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_lay
         io.py = py0 + (l & 1u) * 8u * lx_pad(d.D);
         io.abort = cnt + 8 * CHAIN_FLAGS;
         io.abort_val = ep0 + 1u;
-        to |= moe_layer_step<CPL, VPL, SEG, DR, RB, NW>(d, L, io, lx, tag, ids_out + l * d.K, w_out + l * d.K,
-                                                         n_up, n_down, t, x, nbx);
+        to |= moe_layer_step<CPL, VPL, SEG, DR, RB, NW, true>(d, L, io, lx, tag, ids_out + l * d.K,
+                                                               w_out + l * d.K, n_up, n_down, t, x, nbx);
     }
     // wave 0 of XCD 0 advances the epoch once its last combine is done (that
     // needs every wave's last partials)
