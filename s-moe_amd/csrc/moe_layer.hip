@@ -132,7 +132,14 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     constexpr int NG = WAVE / GL;      // down groups per wave
     constexpr int RW = NG * DR;        // down rows per wave
     constexpr int SH = SEG - ilog2(DR);
-    const int lane = threadIdx.x & (WAVE - 1);
+    // (in the chain of the wide family, opaque per layer: values derived from
+    // the lane are then recomputed per layer instead of hoisted out of the
+    // layer loop and held in registers across it, which left too few for the
+    // top-k proposal below; the narrow family measured 0.5 % faster with them
+    // hoisted)
+    int lane_ = threadIdx.x & (WAVE - 1);
+    if constexpr (CHAIN && CPL == 2) asm volatile("" : "+v"(lane_));
+    const int lane = lane_;
     const uint32_t wv = NW > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0u;
     const uint32_t D = d.D, nch = D >> 5;
     uint64_t* logc = lx + LX_HEAD + x * lx_pad(d.E);
@@ -332,9 +339,8 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     // top-k: the expert of rank x as the top-k network proposes it (E <= 128),
     // so its weights are requested while the softmax and the check run: the
     // narrow configurations, and the wide ones with 6 rows a wave (two waves
-    // a SIMD) outside the chain (whose layer loop leaves too few registers).
-    // Otherwise (more experts, or 8 wide rows) the exact top-k first.
-    constexpr bool PROPOSE = VPL == 2 && (RB * CPL * 2 * 4 <= 64 || (CPL == 2 && RB == 6 && !CHAIN));
+    // a SIMD).  Otherwise (more experts, or 8 wide rows) the exact top-k first.
+    constexpr bool PROPOSE = VPL == 2 && (RB * CPL * 2 * 4 <= 64 || (CPL == 2 && RB == 6));
     uint32_t prop, expert;
     NetTopk net;
     if constexpr (PROPOSE) {
