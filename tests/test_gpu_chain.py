@@ -119,10 +119,18 @@ def test_chain_repeated_calls_shape_change_and_graph_replay(ctx, chain):
         assert torch.equal(junk, ref)
 
 
-def test_chain_235b_shape_equals_layer_calls(ctx, chain):
+@pytest.mark.parametrize("ties", [False, True])
+def test_chain_235b_shape_equals_layer_calls(ctx, chain, ties):
     """At the 235B shape the chain engine runs one chained launch and equals
-    the per-layer launches bit for bit."""
+    the per-layer launches bit for bit; also with router rows duplicated in
+    pairs (exact logit ties at every rank boundary, where the proposed ranks
+    give way to the exact selection)."""
     layers = [Layer(ctx, 4096, 128, 8, 1536, layer_id=240 + i, host=False) for i in range(3)]
+    if ties:
+        for l in layers:
+            rows = l.router.view(128, 4096)
+            rows[1::2] = rows[0::2]
+        torch.cuda.synchronize()
     x0 = hidden_states(ctx, 1, 4096, 34)[0]
     a = x0.clone()
     ctx.profile_enable(True)

@@ -66,6 +66,36 @@ def test_layer_vs_oracle(ctx, oracle, D, E, K, I):
 
 
 @pytest.mark.parametrize("D,E,K,I", [(2048, 128, 8, 768), (4096, 128, 8, 1536)])
+def test_layer_router_ties(ctx, oracle, D, E, K, I):
+    """Router rows duplicated in pairs (experts 2j and 2j + 1, and a triple at
+    0, 1, 2) give exactly equal logits, so every rank boundary is a tie.  The
+    one-launch kernel's proposed ranks cannot be trusted there: the exact
+    selection (scout.cpp:77-123) decides, and any gate/up rows requested for an
+    overturned proposal are requested again for the selected expert.  Ids
+    bit-exact against the oracle, hidden within the tolerance, at both Qwen3
+    shapes (the two families of the kernel)."""
+    layer = Layer(ctx, D, E, K, I, layer_id=D + I + 17, host=False)
+    rows = layer.router.view(E, D)
+    rows[1::2] = rows[0::2]
+    rows[2] = rows[0]
+    layer.host_copies()
+    for index0 in (21, 22, 23):
+        hid = hidden_states(ctx, 1, D, index0)[0]
+        h0 = hid.cpu().numpy()
+        n_layer, n_up = layer_launches(ctx, lambda: decode(ctx, layer, hid))
+        assert n_layer == 1 and n_up == 0, (n_layer, n_up)
+        gids, gw = decode(ctx, layer, hid.copy_(torch.from_numpy(h0).cuda()))
+        out, oid, ow, logits, normed, yo = layer.oracle_decode(oracle, h0)
+        assert (gids == oid).all(), (gids, oid)
+        assert np.allclose(gw, ow, rtol=1e-5, atol=1e-7)
+        got = hid.cpu().numpy()
+        e1, _ = moe_delta_err(got, h0, yo, ow)
+        e2, _ = rel_err(got, out)
+        print(f"{D}x{E}x{K}x{I} ties: ids {gids.tolist()} rel_err delta={e1:.2e} hidden={e2:.2e}")
+        assert max(e1, e2) <= TOL
+
+
+@pytest.mark.parametrize("D,E,K,I", [(2048, 128, 8, 768), (4096, 128, 8, 1536)])
 def test_layer_against_fp64(ctx, D, E, K, I):
     """The one-launch decode layer against an fp64 evaluation of the block
     (same ids and weights), at both Qwen3 shapes: the digit dot products and
