@@ -731,12 +731,14 @@ struct LayerCfg {
     uint32_t n_up, n_down, nbx;
 };
 
-// Waves per block where the block shares its loads: the wide (235B) family,
-// one block per CU of all the CU's waves, 8 or 6 (each wave would otherwise
+// Waves per block where the block shares its loads, one block per CU of all
+// the CU's waves: the wide (235B) family, 8 or 6 (each wave would otherwise
 // read 24 KB of hidden state and norm weights: 28.3 against 29.7 us per layer
-// with 6).  At the 30B shape sharing measured no gain, and one-wave blocks
-// are kept.
-constexpr bool shares_loads(int cpl, int seg) { return cpl == 2 && seg == 6; }
+// with 6), and the narrow (30B) family in the chained kernel, 4 (the block
+// reads the XCD's copy of the input once and polls its flags and the h copy
+// with one wave's share each: 1772 against 1755 tok/s; the one-launch layer
+// kernel keeps one-wave blocks, 1 % faster there).
+constexpr bool shares_loads(int cpl, int seg) { return (cpl == 2 && seg == 6) || (cpl == 1 && seg == 5); }
 
 template <int CPL, int VPL, int SEG, int DR, int RB, bool CHAIN, int NW>
 auto kernel_of()
@@ -850,7 +852,9 @@ hipError_t launch_nw(const LayerCfg& c, const MoeDims& d, const LaunchArgs& a, h
 template <int CPL, int VPL, int SEG, int DR, int RB>
 hipError_t launch_cfg(const LayerCfg& c, const MoeDims& d, const LaunchArgs& a, bool chain, hipStream_t s, bool dry)
 {
-    if constexpr (shares_loads(CPL, SEG)) {
+    if constexpr (shares_loads(CPL, SEG) && CPL == 1) {
+        if (chain && c.nbx % 4 == 0) return launch_nw<CPL, VPL, SEG, DR, RB, true, 4>(c, d, a, s, dry);
+    } else if constexpr (shares_loads(CPL, SEG)) {
         // a block of shared loads where the grid divides into them (one per CU:
         // 256 or 192 waves an XCD)
         if (c.nbx % 8 == 0)
