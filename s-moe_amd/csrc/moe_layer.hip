@@ -370,6 +370,13 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     // wide configurations load each lane's scale beside its row piece (the
     // LDS hand-over costs the 235B layer 2.8 us).
     constexpr bool GATHER = PROPOSE && CPL == 1;
+    // DFIRST (the same, narrow configurations with 16 down rows a wave, in
+    // the chain): the down rows are requested first, ahead of the gate/up
+    // rows, so that they have landed when h is published and polled (loads
+    // complete in order: requested after the h publication, they held back
+    // its poll by their latency).  30B chain 1767 -> 1803 tok/s; the
+    // one-launch layer kernel measured 5 % slower with it (1666 -> 1589).
+    constexpr bool DFIRST = GATHER && SEG == 5 && CHAIN;
     constexpr uint32_t DN_MAX_I = SEG == 5 ? 1024u : 2048u;
     constexpr int NSD = GATHER ? (RW * DN_MAX_I / 512 + WAVE - 1) / WAVE : 1;   // down scale pieces per lane
     const uint32_t nsq_up = RB * D / 512, nsq_dn = RW * d.I / 512;
@@ -425,6 +432,8 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     };
     const uint8_t* blob;
     if constexpr (PROPOSE) {
+        if constexpr (DFIRST)
+            if (t < n_down) issue_down(L.experts + static_cast<size_t>(prop) * L.stride);
         if (t < n_up) issue_up(L.experts + static_cast<size_t>(prop) * L.stride);
         __builtin_amdgcn_sched_barrier(0);
         // the rest of the top-k while the rows land
@@ -434,7 +443,11 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
         blob = L.experts + static_cast<size_t>(expert) * L.stride;
         // a proposal the exact selection overturned (ties, values equal
         // after rounding): the rows again, of the selected expert
-        if (expert != prop && t < n_up) issue_up(blob);
+        if (expert != prop) {
+            if constexpr (DFIRST)
+                if (t < n_down) issue_down(blob);
+            if (t < n_up) issue_up(blob);
+        }
     } else {
         expert = prop;
         blob = L.experts + static_cast<size_t>(prop) * L.stride;
@@ -499,7 +512,8 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
         // the CU has queued ahead of it, so a publication behind these rows
         // would wait for them; issued with the gate/up rows, or once those
         // have landed, they delay h by more than they save)
-        if (t < n_down) issue_down(blob);
+        if constexpr (!DFIRST)
+            if (t < n_down) issue_down(blob);
         // passes of words per lane, every load of a pass in flight before any
         // is checked
         if constexpr (NW > 1) {
