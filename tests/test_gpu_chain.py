@@ -119,19 +119,21 @@ def test_chain_repeated_calls_shape_change_and_graph_replay(ctx, chain):
         assert torch.equal(junk, ref)
 
 
+@pytest.mark.parametrize("D,I", [(4096, 1536), (2048, 768)])
 @pytest.mark.parametrize("ties", [False, True])
-def test_chain_235b_shape_equals_layer_calls(ctx, chain, ties):
-    """At the 235B shape the chain engine runs one chained launch and equals
+def test_chain_shapes_equal_layer_calls(ctx, chain, D, I, ties):
+    """At both Qwen3 shapes the chain engine runs one chained launch and equals
     the per-layer launches bit for bit; also with router rows duplicated in
     pairs (exact logit ties at every rank boundary, where the proposed ranks
-    give way to the exact selection)."""
-    layers = [Layer(ctx, 4096, 128, 8, 1536, layer_id=240 + i, host=False) for i in range(3)]
+    give way to the exact selection and rows requested for an overturned
+    proposal, down rows first in the 30B chain, are requested again)."""
+    layers = [Layer(ctx, D, 128, 8, I, layer_id=240 + i + I, host=False) for i in range(3)]
     if ties:
         for l in layers:
-            rows = l.router.view(128, 4096)
+            rows = l.router.view(128, D)
             rows[1::2] = rows[0::2]
         torch.cuda.synchronize()
-    x0 = hidden_states(ctx, 1, 4096, 34)[0]
+    x0 = hidden_states(ctx, 1, D, 34)[0]
     a = x0.clone()
     ctx.profile_enable(True)
     aids, aw = run_stack(ctx, layers, a)
