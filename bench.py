@@ -841,7 +841,7 @@ def rocprof_summary(d, config, pmc_out, copy_mib, workload="decode"):
     data = json.load(open(pmc_out)) if os.path.exists(pmc_out) else {}
     if workload in GROUPED:
         ent = data.setdefault(GROUPED[workload]["workload"], {})
-        symbols = ("k_grouped_mm<true>", "k_grouped_mm<false>")
+        symbols = ("k_grouped_mm<true>", "k_grouped_down", "k_grouped_mm<false>")
     else:
         ent = data.setdefault(CONFIGS[config]["workload"], {})
         symbols = tuple(KERNEL_SYMBOLS.values())

@@ -52,6 +52,7 @@ struct PrefillScratch {
     uint32_t* ids = nullptr;        // [T x K]
     float* w = nullptr;             // [T x K]
     uint32_t* offsets = nullptr;    // [E + 1]
+    uint32_t* sched = nullptr;      // [E + 1] grouped GEMM work order
     uint32_t* pairs = nullptr;      // [P] sorted pair ids
     float* h = nullptr;             // [P x I]
     uint16_t* h_hi = nullptr;       // [P x I] f16
@@ -181,6 +182,7 @@ void free_prefill_scratch(PrefillScratch& s)
     dfree(s.ids);
     dfree(s.w);
     dfree(s.offsets);
+    dfree(s.sched);
     dfree(s.pairs);
     dfree(s.h);
     dfree(s.h_hi);
@@ -273,6 +275,7 @@ int ensure_prefill_scratch(SmoeMetalCtx* ctx, const SmoeMoeShape* s, uint32_t T)
     const bool ok = dalloc(ctx, &n.x_hi, T_ * n.D) &&
                     dalloc(ctx, &n.x_lo, T_ * n.D) && dalloc(ctx, &n.x_sc, T_) &&
                     dalloc(ctx, &n.ids, P) && dalloc(ctx, &n.w, P) && dalloc(ctx, &n.offsets, size_t(n.E) + 1) &&
+                    dalloc(ctx, &n.sched, size_t(n.E) + 1) &&
                     dalloc(ctx, &n.pairs, P) && dalloc(ctx, &n.h, P * n.I) && dalloc(ctx, &n.h_hi, P * n.I) &&
                     dalloc(ctx, &n.h_lo, P * n.I) && dalloc(ctx, &n.h_sc, P) && dalloc(ctx, &n.y, P * n.D) &&
                     dalloc(ctx, &n.logits, T_ * n.E) && dalloc(ctx, &n.rt_ctr, T_) &&
@@ -988,15 +991,15 @@ extern "C" int smoe_hip_moe_prefill(SmoeMetalCtx* ctx, const SmoeMoeShape* shape
                    }) ||
             !timed(ctx, SMOE_KERNEL_PERMUTE, "permute", [&] {
                 return smoe::launch_permute(ids, w, P, d.K, d.E, offs, s.pairs, sorted_tokens, nullptr, union_ids,
-                                            union_size, ctx->d_err, st);
+                                            union_size, s.sched, ctx->d_err, st);
             }) ||
             !timed(ctx, SMOE_KERNEL_GROUPED_GATE_UP, "grouped_gate_up", [&] {
-                return smoe::launch_grouped_gate_up(d, L, offs, s.pairs, s.x_hi, s.x_lo, s.x_sc, s.h, st);
+                return smoe::launch_grouped_gate_up(d, L, offs, s.sched, s.pairs, s.x_hi, s.x_lo, s.x_sc, s.h, st);
             }) ||
             !timed(ctx, SMOE_KERNEL_SPLIT, "split(h)",
                    [&] { return smoe::launch_split_rows(s.h, P, d.I, s.h_hi, s.h_lo, s.h_sc, st); }) ||
             !timed(ctx, SMOE_KERNEL_GROUPED_DOWN, "grouped_down", [&] {
-                return smoe::launch_grouped_down(d, L, offs, s.pairs, s.h_hi, s.h_lo, s.h_sc, s.y, st);
+                return smoe::launch_grouped_down(d, L, offs, s.sched, s.pairs, s.h_hi, s.h_lo, s.h_sc, s.y, st);
             }) ||
             !timed(ctx, SMOE_KERNEL_SCATTER, "combine",
                    [&] { return smoe::launch_combine_pairs(s.y, w, T, d.K, d.D, hv, st); }))
@@ -1057,7 +1060,7 @@ extern "C" int smoe_hip_permute(SmoeMetalCtx* ctx, const uint32_t* ids, const fl
                  [&] {
                      return smoe::launch_permute(ids, weights, static_cast<uint32_t>(P), top_k, n_experts,
                                                  expert_offsets, ctx->perm_pairs, sorted_tokens, sorted_weights,
-                                                 union_ids, union_size, ctx->d_err, ctx->stream);
+                                                 union_ids, union_size, nullptr, ctx->d_err, ctx->stream);
                  })
                ? SMOE_OK
                : SMOE_ERR_HIP;

@@ -223,20 +223,23 @@ hipError_t launch_split_rows(const float* src, uint32_t rows, uint32_t cols, uin
                              float* scale, hipStream_t s);
 // Stable counting sort of the P pairs by expert: offsets [E+1],
 // sorted_pairs [P] (pair = token * K + rank); sorted_tokens, sorted_w,
-// union_ids [E], union_size [1] optional (nullptr).  Bad ids set err bit 1.
+// union_ids [E], union_size [1] optional (nullptr).  sched [E + 1] optional: the
+// grouped GEMMs' work order (count of touched experts, then the experts by
+// decreasing cost).  Bad ids set err bit 1.
 constexpr size_t PERMUTE_MAX_LDS = 48 * 1024;
 size_t permute_lds_bytes(uint32_t P, uint32_t E);
 hipError_t launch_permute(const uint32_t* ids, const float* w, uint32_t P, uint32_t K, uint32_t E, uint32_t* offsets,
                           uint32_t* sorted_pairs, uint32_t* sorted_tokens, float* sorted_w, uint32_t* union_ids,
-                          uint32_t* union_size, uint32_t* err, hipStream_t s);
+                          uint32_t* union_size, uint32_t* sched, uint32_t* err, hipStream_t s);
 // Grouped expert GEMMs over the permuted pairs (MFMA f16, hi/lo activations):
-// h [P x I] = silu(x G^T) * (x U^T); y [P x D] = h Dn^T.
+// h [P x I] = silu(x G^T) * (x U^T); y [P x D] = h Dn^T.  sched is the
+// permute's work order.
 hipError_t launch_grouped_gate_up(const MoeDims& d, const LayerDesc& L, const uint32_t* offsets,
-                                  const uint32_t* sorted_pairs, const uint16_t* x_hi, const uint16_t* x_lo,
-                                  const float* x_scale, float* h, hipStream_t s);
+                                  const uint32_t* sched, const uint32_t* sorted_pairs, const uint16_t* x_hi,
+                                  const uint16_t* x_lo, const float* x_scale, float* h, hipStream_t s);
 hipError_t launch_grouped_down(const MoeDims& d, const LayerDesc& L, const uint32_t* offsets,
-                               const uint32_t* sorted_pairs, const uint16_t* h_hi, const uint16_t* h_lo,
-                               const float* h_scale, float* y, hipStream_t s);
+                               const uint32_t* sched, const uint32_t* sorted_pairs, const uint16_t* h_hi,
+                               const uint16_t* h_lo, const float* h_scale, float* y, hipStream_t s);
 // hidden[t] += sum_r w[t][r] * y[t*K + r] (rank order).
 hipError_t launch_combine_pairs(const float* y, const float* w, uint32_t T, uint32_t K, uint32_t D, float* hidden,
                                 hipStream_t s);

@@ -297,15 +297,21 @@ void k_split_rows(const float* __restrict__ src, uint32_t rows, uint32_t cols, u
 // each pair's slot = prefix + its rank among equal ids earlier in the chunk.
 // Union order (first appearance, token-major, prefill.cpp:55-68) ranks the
 // touched experts by their first pair.  ids >= E are skipped and flagged in
-// err (bit 1).
+// err (bit 1).  sched (optional, [E + 1]) receives the grouped GEMMs' work
+// order: sched[0] = number of touched experts, then the touched experts by
+// decreasing cost (gm_cost of their pair count), ties by expert id.
 // ---------------------------------------------------------------------------
 constexpr int PERM_THREADS = 1024;
+
+// relative cost of one (expert, row tile) block of the grouped GEMMs with M
+// pairs: a fixed share per pass of up to 64 pairs plus one per 16-pair m-tile
+__device__ __forceinline__ uint32_t gm_cost(uint32_t M) { return 2u * ((M + 63u) >> 6) + ((M + 15u) >> 4); }
 
 __global__ __launch_bounds__(PERM_THREADS)
 void k_permute(const uint32_t* __restrict__ ids, const float* __restrict__ w, uint32_t P, uint32_t K, uint32_t E,
                uint32_t* __restrict__ offsets, uint32_t* __restrict__ sorted_pairs,
                uint32_t* __restrict__ sorted_tokens, float* __restrict__ sorted_w, uint32_t* __restrict__ union_ids,
-               uint32_t* __restrict__ union_size, uint32_t* __restrict__ err)
+               uint32_t* __restrict__ union_size, uint32_t* __restrict__ sched, uint32_t* __restrict__ err)
 {
     extern __shared__ uint32_t s_mem[];
     const uint32_t C = (P + 63) / 64;
@@ -445,6 +451,32 @@ void k_permute(const uint32_t* __restrict__ ids, const float* __restrict__ w, ui
         for (uint32_t e = 0; e < E; ++e) n += s_tot[e] != 0;
         *union_size = n;
     }
+    // GEMM work order: rank of each touched expert by (cost descending, id).  S
+    // threads (a power of two, in one wave) share an expert's comparisons, as in
+    // the prefix above, and sum their counts with shuffles.
+    if (sched) {
+        uint32_t S = 64;
+        while (S > 1 && E * S > PERM_THREADS) S >>= 1;
+        const uint32_t e = threadIdx.x / S, sg = threadIdx.x % S;
+        uint32_t r = 0, n = 0, m = 0;
+        if (e < E) {
+            m = s_tot[e];
+            const uint32_t ce = gm_cost(m);
+            for (uint32_t e2 = sg; e2 < E; e2 += S) {
+                const uint32_t m2 = s_tot[e2], c2 = gm_cost(m2);
+                n += m2 != 0;
+                r += m2 != 0 && (c2 > ce || (c2 == ce && e2 < e));
+            }
+        }
+        for (uint32_t dlt = 1; dlt < S; dlt <<= 1) {
+            r += __shfl_xor(r, dlt, S);
+            n += __shfl_xor(n, dlt, S);
+        }
+        if (e < E && sg == 0) {
+            if (m != 0) sched[1 + r] = e;
+            if (e == 0) sched[0] = n;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -453,7 +485,12 @@ void k_permute(const uint32_t* __restrict__ ids, const float* __restrict__ w, ui
 // (gate+up, SiLU fused) or 256 rows of down.  Block = 8 waves; wave w owns two
 // 16-row MFMA subtiles (gate and up rows 16w.., or down rows 32w.. and
 // 32w + 16..) and all m-tiles of the pass (up to 64 pairs, so each weight is
-// read once per expert for M <= 64).
+// read once per expert for M <= 64).  Block b works on the schedule's rank
+// r = 8 s + x (s even) or 8 s + 7 - x (s odd) for x = b mod 8 (its XCD under
+// the round-robin deal) and slot s = (b / 8) / n_tiles, tile (b / 8) mod
+// n_tiles: every tile of an expert runs on one XCD (the activation rows stay
+// in its L2), and the experts, dealt in decreasing cost down and up the XCDs,
+// leave every XCD about the same work whatever the routing.
 //
 // The k dimension streams through two rings in LDS, filled by direct
 // global->LDS loads (global_load_lds_dwordx4) so that nothing in flight holds
@@ -464,8 +501,9 @@ void k_permute(const uint32_t* __restrict__ ids, const float* __restrict__ w, ui
 //                and the rows' two fp16 scales;
 //   activations  GM_SA stages of one group: the pass's rows (f16 hi and lo
 //                planes), a share per wave.
-// Body c (one group) waits for its stages, passes one barrier, requests weight
-// stage c/2 + 3 (even c) and activation stage c + 3, and computes.  Each stage
+// Body c (one group) waits for its stages, passes one barrier, requests
+// activation stage c + 3 and then (even c) weight stage c/2 + 3, and computes:
+// the weights, from HBM, then have five bodies before a wait covers them.  Each stage
 // lives in its own __shared__ object, so the compiler can tell the in-flight
 // fills from the stage being read; completion is awaited with an explicit
 // vmcnt: every wave issues the same loads in the same order.
@@ -625,27 +663,32 @@ __device__ __forceinline__ void grouped_mm_expert(
 #pragma unroll
             for (int j = 0; j < 2; ++j) acc[ms][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-        // Issue order of the loop: body c issues the weight stage c / 2 + 3 (if c is even)
-        // and then the activation stage c + 3.  The prologue replays bodies -6 .. -1.
+        // Issue order of the loop: body c issues the activation stage c + 3 and then the
+        // weight stage c / 2 + 3 (if c is even).  The prologue replays bodies -6 .. -1.
         const uint32_t NWS = (G + 1) / 2;        // weight stages
         if (0 < NWS) issue_w(w0, 0);
         if (1 < NWS) issue_w(w1, 1);
         if (0 < G) issue_a(a0, 0);
-        if (2 < NWS) issue_w(w2, 2);
         if (1 < G) issue_a(a1, 1);
+        if (2 < NWS) issue_w(w2, 2);
         if (2 < G) issue_a(a2, 2);
         mem_fence_compiler();
 
         auto body = [&](uint32_t c, GmW& W, uint32_t g, GmW& WN, GmA& A, GmA& AN_) {
-            // A(c) was the last load of body c - 3; bodies c - 2 and c - 1 issued A(c + 1),
-            // A(c + 2) and, in the even one of them, the weight stage (c + 4 + (c & 1)) / 2.
-            // When all of those were issued, 2 AN + 3 loads may still be pending; near the
-            // end fewer were, and the wait covers everything.
-            if (c + 2 < G && (c + 4 + (c & 1)) / 2 < NWS) vm_wait<2 * AN + 3>();
-            else vm_wait<0>();
+            // A(c) was the first load of body c - 3; after it came the weight stage of body
+            // c - 3 when c - 3 is even, A(c + 1), A(c + 2) and the weight stage of the even
+            // one of bodies c - 2, c - 1 ((c + 4 + (c & 1)) / 2, the later of the two).  When
+            // all of those were issued, 2 AN + 3 (even c) or 2 AN + 6 (odd c) loads may still
+            // be pending; near the end fewer were, and the wait covers everything.
+            if (c + 2 < G && (c + 4 + (c & 1)) / 2 < NWS) {
+                if (g) vm_wait<2 * AN + 6>();
+                else vm_wait<2 * AN + 3>();
+            } else {
+                vm_wait<0>();
+            }
             gm_barrier();
-            if (g == 0 && c / 2 + 3 < NWS) issue_w(WN, c / 2 + 3);
             if (c + 3 < G) issue_a(AN_, c + 3);
+            if (g == 0 && c / 2 + 3 < NWS) issue_w(WN, c / 2 + 3);
             mem_fence_compiler();
             half8_t b[2][2];
             float sc[2];
@@ -715,7 +758,7 @@ __device__ __forceinline__ void grouped_mm_expert(
 template <bool GATE_UP>
 __global__ __launch_bounds__(GM_WAVES * WAVE, 1)
 void k_grouped_mm(MoeDims d, LayerDesc L, const uint32_t* __restrict__ offsets,
-                  const uint32_t* __restrict__ sorted_pairs, const uint16_t* __restrict__ a_hi,
+                  const uint32_t* __restrict__ sched, const uint32_t* __restrict__ sorted_pairs, const uint16_t* __restrict__ a_hi,
                   const uint16_t* __restrict__ a_lo, const float* __restrict__ a_scale, uint32_t a_row_div,
                   float* __restrict__ out, uint32_t n_dim, uint32_t k_dim, uint32_t n_tiles)
 {
@@ -724,7 +767,10 @@ void k_grouped_mm(MoeDims d, LayerDesc L, const uint32_t* __restrict__ offsets,
     __shared__ uint32_t s_row[GM_PASS];
     __shared__ uint32_t s_pair[GM_PASS];
     const uint32_t b = blockIdx.x, xcd = b & 7u, jb = b >> 3;
-    const uint32_t e = xcd + 8u * (jb / n_tiles), tile = jb % n_tiles;
+    const uint32_t slot = jb / n_tiles, tile = jb % n_tiles;
+    const uint32_t r = 8u * slot + ((slot & 1u) ? 7u - xcd : xcd);
+    if (r >= sched[0]) return;
+    const uint32_t e = sched[1 + r];
     if (e >= d.E) return;
     const uint32_t base = offsets[e], M = offsets[e + 1] - base;
     if (M == 0) return;
@@ -740,6 +786,241 @@ void k_grouped_mm(MoeDims d, LayerDesc L, const uint32_t* __restrict__ offsets,
     else
         grouped_mm_expert<GATE_UP, 4>(d, L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, a_row_div, out,
                                       n_dim, k_dim, w0, w1, w2, w3, a0, a1, a2, a3, s_row, s_pair);
+}
+
+// ---------------------------------------------------------------------------
+// k_grouped_down: the down products of k_grouped_mm<false> (same pairs, same
+// sums per 64-column group, same epilogue) with the weights streamed into
+// registers: each weight row belongs to one wave, so plain loads need neither
+// LDS nor a barrier for them.  Blocks of 4 waves x 64 rows (four 16-row
+// subtiles a wave), two blocks per CU: every activation fragment read from LDS
+// feeds four subtiles (half the LDS reads per weight of the 8 x 32-row block),
+// and the two blocks of a CU pass their barriers independently, so one block's
+// MFMAs overlap the other's conversion.  Needs an even number of groups (a
+// stage's two scales are one dword); at the Qwen3 shapes it takes 66 us
+// against 79 for k_grouped_mm<false> (30B, 512 tokens).
+//   weights  per wave and stage (two groups: 64 bytes of every row), subtile
+//            j: lane l loads row l & 15, bytes 16 (l >> 4) .. + 15; one
+//            v_permlane32_swap per two dwords then leaves every lane one dword
+//            of each (group, MFMA step): quad q, step s of either group holds
+//            its 8-column unit 4 (q & 1) + 2 (q >> 1) + s, and the activation
+//            fragments are read from those units;
+//   acts     the ring of k_grouped_mm (f16 hi/lo planes, XOR-swizzled 16-byte
+//            slots), filled by direct loads issued from inline asm: the
+//            compiler does not track them, so it adds no waits of its own for
+//            the ring (it would drain every load in flight once per unrolled
+//            iteration); the explicit vmcnt waits cover them.
+// ---------------------------------------------------------------------------
+constexpr int GD_WAVES = 4;
+constexpr int GD_SUB = 4;                                  // 16-row subtiles a wave
+constexpr uint32_t GD_ROWS = 16 * GD_SUB * GD_WAVES;       // down rows per block
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p)
+{
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+// lane l's 16 bytes land at LDS byte address lds + 16 l
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+
+template <int MS>
+__device__ __forceinline__ void grouped_down_expert(
+    const LayerDesc& L, uint32_t e, uint32_t tile, uint32_t base, uint32_t M, const uint32_t* __restrict__ sorted_pairs,
+    const uint16_t* __restrict__ a_hi, const uint16_t* __restrict__ a_lo, const float* __restrict__ a_scale,
+    float* __restrict__ out, uint32_t n_dim, uint32_t k_dim, GmA& a0, GmA& a1, GmA& a2, GmA& a3,
+    uint32_t (&s_row)[GM_PASS], uint32_t (&s_pair)[GM_PASS])
+{
+    constexpr int AN = MS;                       // activation loads per wave and stage (4 rows each)
+    constexpr int PASS = 16 * MS;
+    constexpr int WS = 2 * GD_SUB;               // loads per weight stage (codes, scales)
+    const int lane = threadIdx.x & 63;
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t G = k_dim >> 6, NWS = G / 2;
+    const uint32_t m16 = lane & 15, q = lane >> 4;
+
+    const uint8_t* blob = L.experts + static_cast<size_t>(e) * L.stride;
+    const size_t row_bytes = k_dim >> 1;
+    const uint8_t* w_src[GD_SUB];
+    const uint32_t* s_src[GD_SUB];
+#pragma unroll
+    for (int j = 0; j < GD_SUB; ++j) {
+        const uint32_t r = min(tile * GD_ROWS + 16 * GD_SUB * wv + 16 * j + m16, n_dim - 1);
+        w_src[j] = blob + L.off[4] + static_cast<size_t>(r) * row_bytes + 16 * q;
+        s_src[j] = reinterpret_cast<const uint32_t*>(blob + L.off[5] + static_cast<size_t>(r) * G * 2);
+    }
+    uint4 wr[4][GD_SUB];                         // weight ring: [stage slot][subtile]
+    uint32_t sr[4][GD_SUB];                      // the stage's two fp16 scales per subtile
+    auto issue_w = [&](int slot, uint32_t st) {
+#pragma unroll
+        for (int j = 0; j < GD_SUB; ++j) wr[slot][j] = *reinterpret_cast<const uint4*>(w_src[j] + 64 * st);
+#pragma unroll
+        for (int j = 0; j < GD_SUB; ++j) sr[slot][j] = s_src[j][st];
+    };
+    uint32_t aoff[2][2];
+    const uint32_t u8 = 4 * (q & 1) + 2 * (q >> 1);
+#pragma unroll
+    for (int stp = 0; stp < 2; ++stp)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) aoff[stp][pl] = m16 * 256 + 16 * ((8 * pl + u8 + stp) ^ m16);
+
+    for (uint32_t m0 = 0; m0 < M; m0 += PASS) {
+        __syncthreads();
+        if (threadIdx.x < PASS) {
+            const uint32_t p = sorted_pairs[base + min(m0 + threadIdx.x, M - 1)];
+            s_pair[threadIdx.x] = p;
+            s_row[threadIdx.x] = p;
+        }
+        __syncthreads();
+        const uint16_t* a_src[AN];
+#pragma unroll
+        for (int u = 0; u < AN; ++u) {
+            const uint32_t r = wv * 4 * AN + 4 * u + (lane >> 4);
+            const uint32_t x = (lane & 15) ^ (r & 15);
+            const uint32_t srow = s_row[min(r, static_cast<uint32_t>(PASS - 1))];
+            a_src[u] = ((x >> 3) ? a_lo : a_hi) + static_cast<size_t>(srow) * k_dim + 8 * (x & 7);
+        }
+        auto issue_a = [&](GmA& S, uint32_t c) {
+#pragma unroll
+            for (int u = 0; u < AN; ++u) dma16(a_src[u] + c * 64, lds_addr(&S.a[(wv * 4 * AN + 4 * u) * 256]));
+        };
+
+        f32x4_t acc[MS][GD_SUB];
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+            for (int j = 0; j < GD_SUB; ++j) acc[ms][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+        // body c issues the activation stage c + 3 and then (even c) the weight
+        // stage c / 2 + 3; the prologue replays bodies -6 .. -1
+        if (0 < NWS) issue_w(0, 0);
+        if (1 < NWS) issue_w(1, 1);
+        issue_a(a0, 0);
+        if (1 < G) issue_a(a1, 1);
+        if (2 < NWS) issue_w(2, 2);
+        if (2 < G) issue_a(a2, 2);
+        mem_fence_compiler();
+
+        uint32_t gw[GD_SUB][2][2];               // [subtile][group of the stage][MFMA step]
+        auto body = [&](uint32_t c, int slot, int g, int nslot, GmA& A, GmA& AN_) {
+            // After A(c) (first load of body c - 3) came: the weight stage of body c - 3
+            // when c - 3 is even, A(c + 1), A(c + 2) and the weight stage of the even one
+            // of bodies c - 2, c - 1.  When all of those were issued, 2 AN + WS (even c)
+            // or 2 AN + 2 WS (odd c) loads may still be pending; near the end fewer
+            // were, and the wait covers everything.  A(c) done also means the weight
+            // stage c / 2 is: it was issued in body c - 6, before A(c).
+            if (c + 2 < G && (c + 4 + (c & 1)) / 2 < NWS) {
+                if (g) vm_wait<2 * AN + 2 * WS>();
+                else vm_wait<2 * AN + WS>();
+            } else {
+                vm_wait<0>();
+            }
+            gm_barrier();
+            if (c + 3 < G) issue_a(AN_, c + 3);
+            if (g == 0 && c / 2 + 3 < NWS) issue_w(nslot, c / 2 + 3);
+            mem_fence_compiler();
+            if (g == 0) {
+#pragma unroll
+                for (int j = 0; j < GD_SUB; ++j)
+#pragma unroll
+                    for (int s = 0; s < 2; ++s) {
+                        // lanes 0-31 hold the stage's group 0 (bytes 0-31 of the 64), lanes
+                        // 32-63 group 1: swap dwords 2 + s of the lower half with dwords s
+                        // of the upper half
+                        const uint32_t lo = s ? wr[slot][j].y : wr[slot][j].x;
+                        const uint32_t hi = s ? wr[slot][j].w : wr[slot][j].z;
+                        const auto r = __builtin_amdgcn_permlane32_swap(lo, hi, false, false);
+                        gw[j][0][s] = r[0];
+                        gw[j][1][s] = r[1];
+                    }
+            }
+            half8_t b[GD_SUB][2];
+            float sc[GD_SUB];
+#pragma unroll
+            for (int j = 0; j < GD_SUB; ++j) {
+                b[j][0] = q4_codes_to_f16(gw[j][g][0]);
+                b[j][1] = q4_codes_to_f16(gw[j][g][1]);
+                sc[j] = f16_bits_to_f32(static_cast<uint16_t>(g ? sr[slot][j] >> 16 : sr[slot][j]));
+            }
+#pragma unroll
+            for (int ms = 0; ms < MS; ++ms) {
+                half8_t xa[2][2];
+#pragma unroll
+                for (int stp = 0; stp < 2; ++stp)
+#pragma unroll
+                    for (int pl = 0; pl < 2; ++pl) xa[stp][pl] = lds_half8(A.a + ms * 4096 + aoff[stp][pl]);
+#pragma unroll
+                for (int j = 0; j < GD_SUB; ++j) {
+                    f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[0][0], b[j][0], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[0][1], b[j][0], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1][0], b[j][1], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[1][1], b[j][1], t, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[ms][j][i] = fmaf(sc[j], t[i], acc[ms][j][i]);
+                }
+            }
+            mem_fence_compiler();
+        };
+        for (uint32_t c = 0; c < G; c += 8) {
+            body(c, 0, 0, 3, a0, a3);
+            if (c + 1 < G) body(c + 1, 0, 1, 3, a1, a0);
+            if (c + 2 < G) body(c + 2, 1, 0, 0, a2, a1);
+            if (c + 3 < G) body(c + 3, 1, 1, 0, a3, a2);
+            if (c + 4 < G) body(c + 4, 2, 0, 1, a0, a3);
+            if (c + 5 < G) body(c + 5, 2, 1, 1, a1, a0);
+            if (c + 6 < G) body(c + 6, 3, 0, 2, a2, a1);
+            if (c + 7 < G) body(c + 7, 3, 1, 2, a3, a2);
+        }
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = 16 * ms + 4 * q + i;
+                if (m0 + m >= M) continue;
+                const float rs = a_scale[s_row[m]] * (8.0f / 15.0f);   // weights are (2c - 15) / 8
+                float* o = out + static_cast<size_t>(s_pair[m]) * n_dim;
+#pragma unroll
+                for (int j = 0; j < GD_SUB; ++j) {
+                    const uint32_t n = tile * GD_ROWS + 16 * GD_SUB * wv + 16 * j + m16;
+                    if (n < n_dim) o[n] = acc[ms][j][i] * rs;
+                }
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(GD_WAVES * WAVE, 2)
+void k_grouped_down(MoeDims d, LayerDesc L, const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ sched,
+                    const uint32_t* __restrict__ sorted_pairs, const uint16_t* __restrict__ a_hi,
+                    const uint16_t* __restrict__ a_lo, const float* __restrict__ a_scale, float* __restrict__ out,
+                    uint32_t n_dim, uint32_t k_dim, uint32_t n_tiles)
+{
+    __shared__ __align__(16) GmA a0, a1, a2, a3;
+    __shared__ uint32_t s_row[GM_PASS];
+    __shared__ uint32_t s_pair[GM_PASS];
+    // the schedule order of k_grouped_mm
+    const uint32_t b = blockIdx.x, xcd = b & 7u, jb = b >> 3;
+    const uint32_t slot = jb / n_tiles, tile = jb % n_tiles;
+    const uint32_t r = 8u * slot + ((slot & 1u) ? 7u - xcd : xcd);
+    if (r >= sched[0]) return;
+    const uint32_t e = sched[1 + r];
+    if (e >= d.E) return;
+    const uint32_t base = offsets[e], M = offsets[e + 1] - base;
+    if (M == 0) return;
+    if (M <= 16)
+        grouped_down_expert<1>(L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, out, n_dim, k_dim, a0, a1, a2,
+                               a3, s_row, s_pair);
+    else if (M <= 32)
+        grouped_down_expert<2>(L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, out, n_dim, k_dim, a0, a1, a2,
+                               a3, s_row, s_pair);
+    else if (M <= 48)
+        grouped_down_expert<3>(L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, out, n_dim, k_dim, a0, a1, a2,
+                               a3, s_row, s_pair);
+    else
+        grouped_down_expert<4>(L, e, tile, base, M, sorted_pairs, a_hi, a_lo, a_scale, out, n_dim, k_dim, a0, a1, a2,
+                               a3, s_row, s_pair);
 }
 
 // ---------------------------------------------------------------------------
@@ -831,33 +1112,40 @@ size_t permute_lds_bytes(uint32_t P, uint32_t E)
 
 hipError_t launch_permute(const uint32_t* ids, const float* w, uint32_t P, uint32_t K, uint32_t E, uint32_t* offsets,
                           uint32_t* sorted_pairs, uint32_t* sorted_tokens, float* sorted_w, uint32_t* union_ids,
-                          uint32_t* union_size, uint32_t* err, hipStream_t s)
+                          uint32_t* union_size, uint32_t* sched, uint32_t* err, hipStream_t s)
 {
     const size_t lds = permute_lds_bytes(P, E);
     if (P == 0 || E == 0 || lds > PERMUTE_MAX_LDS) return hipErrorInvalidValue;
     launch_kernel_lds(k_permute, dim3(1), dim3(PERM_THREADS), static_cast<uint32_t>(lds), s, ids, w, P, K, E,
-                      offsets, sorted_pairs, sorted_tokens, sorted_w, union_ids, union_size, err);
+                      offsets, sorted_pairs, sorted_tokens, sorted_w, union_ids, union_size, sched, err);
     return hipGetLastError();
 }
 
 hipError_t launch_grouped_gate_up(const MoeDims& d, const LayerDesc& L, const uint32_t* offsets,
-                                  const uint32_t* sorted_pairs, const uint16_t* x_hi, const uint16_t* x_lo,
-                                  const float* x_scale, float* h, hipStream_t s)
+                                  const uint32_t* sched, const uint32_t* sorted_pairs, const uint16_t* x_hi,
+                                  const uint16_t* x_lo, const float* x_scale, float* h, hipStream_t s)
 {
     if (d.group != 64 || d.I % 64 || d.D % 64) return hipErrorInvalidValue;
     const uint32_t n_tiles = (d.I + GM_ROWS_GU - 1) / GM_ROWS_GU, eg = (d.E + 7) / 8;
-    launch_kernel(k_grouped_mm<true>, dim3(8 * eg * n_tiles), dim3(GM_WAVES * WAVE), s, d, L, offsets, sorted_pairs,
-                  x_hi, x_lo, x_scale, d.K, h, d.I, d.D, n_tiles);
+    launch_kernel(k_grouped_mm<true>, dim3(8 * eg * n_tiles), dim3(GM_WAVES * WAVE), s, d, L, offsets, sched,
+                  sorted_pairs, x_hi, x_lo, x_scale, d.K, h, d.I, d.D, n_tiles);
     return hipGetLastError();
 }
 
 hipError_t launch_grouped_down(const MoeDims& d, const LayerDesc& L, const uint32_t* offsets,
-                               const uint32_t* sorted_pairs, const uint16_t* h_hi, const uint16_t* h_lo,
-                               const float* h_scale, float* y, hipStream_t s)
+                               const uint32_t* sched, const uint32_t* sorted_pairs, const uint16_t* h_hi,
+                               const uint16_t* h_lo, const float* h_scale, float* y, hipStream_t s)
 {
     if (d.group != 64 || d.D % 64 || d.I % 64) return hipErrorInvalidValue;
-    const uint32_t n_tiles = (d.D + GM_ROWS_DN - 1) / GM_ROWS_DN, eg = (d.E + 7) / 8;
-    launch_kernel(k_grouped_mm<false>, dim3(8 * eg * n_tiles), dim3(GM_WAVES * WAVE), s, d, L, offsets,
+    const uint32_t eg = (d.E + 7) / 8;
+    if (d.I % 128 == 0) {                        // an even number of groups: the register-weight kernel
+        const uint32_t nt = (d.D + GD_ROWS - 1) / GD_ROWS;
+        launch_kernel(k_grouped_down, dim3(8 * eg * nt), dim3(GD_WAVES * WAVE), s, d, L, offsets, sched, sorted_pairs,
+                      h_hi, h_lo, h_scale, y, d.D, d.I, nt);
+        return hipGetLastError();
+    }
+    const uint32_t n_tiles = (d.D + GM_ROWS_DN - 1) / GM_ROWS_DN;
+    launch_kernel(k_grouped_mm<false>, dim3(8 * eg * n_tiles), dim3(GM_WAVES * WAVE), s, d, L, offsets, sched,
                   sorted_pairs, h_hi, h_lo, h_scale, 1u, y, d.D, d.I, n_tiles);
     return hipGetLastError();
 }
