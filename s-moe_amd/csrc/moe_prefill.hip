@@ -1125,7 +1125,7 @@ hipError_t launch_grouped_gate_up(const MoeDims& d, const LayerDesc& L, const ui
                                   const uint32_t* sched, const uint32_t* sorted_pairs, const uint16_t* x_hi,
                                   const uint16_t* x_lo, const float* x_scale, float* h, hipStream_t s)
 {
-    if (d.group != 64 || d.I % 64 || d.D % 64) return hipErrorInvalidValue;
+    if (d.group != 64 || d.I % 64 || d.D % 64 || !offsets || !sched) return hipErrorInvalidValue;
     const uint32_t n_tiles = (d.I + GM_ROWS_GU - 1) / GM_ROWS_GU, eg = (d.E + 7) / 8;
     launch_kernel(k_grouped_mm<true>, dim3(8 * eg * n_tiles), dim3(GM_WAVES * WAVE), s, d, L, offsets, sched,
                   sorted_pairs, x_hi, x_lo, x_scale, d.K, h, d.I, d.D, n_tiles);
@@ -1136,7 +1136,7 @@ hipError_t launch_grouped_down(const MoeDims& d, const LayerDesc& L, const uint3
                                const uint32_t* sched, const uint32_t* sorted_pairs, const uint16_t* h_hi,
                                const uint16_t* h_lo, const float* h_scale, float* y, hipStream_t s)
 {
-    if (d.group != 64 || d.D % 64 || d.I % 64) return hipErrorInvalidValue;
+    if (d.group != 64 || d.D % 64 || d.I % 64 || !offsets || !sched) return hipErrorInvalidValue;
     const uint32_t eg = (d.E + 7) / 8;
     if (d.I % 128 == 0) {                        // an even number of groups: the register-weight kernel
         const uint32_t nt = (d.D + GD_ROWS - 1) / GD_ROWS;
