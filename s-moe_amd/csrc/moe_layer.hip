@@ -105,6 +105,7 @@ struct LayerIO {
     uint64_t* py;            // the rank partials' exchange words
     uint32_t* abort;         // null, or: a wave that times out stores abort_val here, and
     uint32_t abort_val;      // every wait ends once it reads abort_val
+    const uint16_t* next_router;   // null, or: the next layer's router rows (touched into the L2)
 };
 
 // a bounded wait's spin count: true once the wait is to end unfinished
@@ -431,11 +432,20 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
         }
     };
     const uint8_t* blob;
+    uint32_t touch = 0;
     if constexpr (PROPOSE) {
         if constexpr (DFIRST)
             if (t < n_down) issue_down(L.experts + static_cast<size_t>(prop) * L.stride);
         if (t < n_up) issue_up(L.experts + static_cast<size_t>(prop) * L.stride);
         __builtin_amdgcn_sched_barrier(0);
+        // the next layer's router row of this wave, one dword of each 128-byte
+        // line into the XCD's L2, behind the expert rows (it lands with them,
+        // before anything this layer waits for is requested)
+        if constexpr (CHAIN && CPL == 1)
+            if (io.next_router && producer) {
+                const uint32_t r = (lane >> 5) && second ? t + nbx : t;
+                touch = io.next_router[static_cast<size_t>(r) * D + min((static_cast<uint32_t>(lane) & 31u) * 64u, D - 1)];
+            }
         // the rest of the top-k while the rows land
         topk_net_finish<VPL>(v, d.E, d.K, d.norm_topk, my_id, my_w, slots, net);
         // (clamped: a timed-out exchange must still index inside the pool)
@@ -653,6 +663,8 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     }
     if (timed_out && io.abort && lane == 0)
         __hip_atomic_store(io.abort, io.abort_val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // (keeps the touch's register until every load of the layer has landed)
+    if constexpr (CHAIN && CPL == 1) asm volatile("" ::"v"(touch));
     return timed_out;
 }
 
@@ -726,6 +738,7 @@ void k_moe_chain(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_lay
         io.py = py0 + (l & 1u) * 8u * lx_pad(d.D);
         io.abort = cnt + 8 * CHAIN_FLAGS;
         io.abort_val = ep0 + 1u;
+        io.next_router = last ? nullptr : layers[l + 1].router_w;
         to |= moe_layer_step<CPL, VPL, SEG, DR, RB, NW, true>(d, L, io, lx, tag, ids_out + l * d.K,
                                                                w_out + l * d.K, n_up, n_down, t, x, nbx);
     }
