@@ -832,8 +832,8 @@ void k_grouped_mm(MoeDims d, LayerDesc L, const uint32_t* __restrict__ offsets,
 // feeds four subtiles (half the LDS reads per weight of the 8 x 32-row block),
 // and the two blocks of a CU pass their barriers independently, so one block's
 // MFMAs overlap the other's conversion.  Needs an even number of groups (a
-// stage's two scales are one dword); at the Qwen3 shapes it takes 66 us
-// against 79 for k_grouped_mm<false> (30B, 512 tokens).
+// stage's two scales are one dword).  30B layer, 512 tokens: 58.9 us against
+// 72 for k_grouped_mm<false> (bench.py --workload prefill).
 //   weights  per wave and stage (two groups: 64 bytes of every row), subtile
 //            j: lane l loads row l & 15, bytes 16 (l >> 4) .. + 15; one
 //            v_permlane32_swap per two dwords then leaves every lane one dword
