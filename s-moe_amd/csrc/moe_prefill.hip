@@ -81,7 +81,11 @@ __device__ __forceinline__ void split8_f16(const float* x, int e, uint4& hi, uin
 // the blocks write their logits with agent-scope stores, wait for them, and
 // add themselves to a device-scope counter per token group; the block that
 // finds the count at ES - 1 modulo ES runs the group's top-k on agent-scope
-// loads of the logits (no device-wide fence anywhere).
+// loads of the logits (no device-wide fence anywhere).  There (one token a
+// block) only wave 0 reads and normalises the token and hands it to the other
+// waves through LDS, and every wave requests its first router rows before
+// that, so the hidden row's and the router rows' round trips overlap (at 64
+// tokens of the 235B shape 16.1 -> 13.3 us, same bits).
 // ---------------------------------------------------------------------------
 constexpr int ROUTE_WAVES = 8;
 
@@ -106,10 +110,123 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
     const uint32_t rows_per = (d.E + ES - 1) / ES, rbeg = eg * rows_per, rend = min(d.E, rbeg + rows_per);
     const uint32_t D = d.D, nch = D >> 5;
 
+    // router rows per load group (see below); with ES > 1 the wave's first
+    // group is requested before the norm
+    constexpr int RG_FIT = (208 - 32 * TB * CPL) / (16 * CPL);
+    constexpr int RG_ALL = RG_FIT >= RPB ? RPB : RG_FIT >= 8 ? 8 : RG_FIT >= 4 ? 4 : RG_FIT >= 2 ? 2 : 1;
+    // (two rows a group where wave 0's hidden chunks are live beside them)
+    constexpr int RG = ES > 1 && CPL > 1 && RG_ALL > 2 ? 2 : RG_ALL;
+    static_assert(RPB % RG == 0, "row groups of a batch");
+    const uint32_t rfirst = rbeg + wv * RPB;
+    uint4 rws[RG][CPL][4];
     float a[TB][CPL][32];
+    if constexpr (ES > 1) {
+        // one token: wave 0 normalises it (and, in the first block, writes its
+        // f16 planes) and hands it to the other waves through LDS; every wave
+        // requests its router rows before that, so the two round trips overlap
+        static_assert(TB == 1, "one token a block when the rows are split");
+        __shared__ __align__(16) float4 s_a[CPL][8][WAVE];
+        float4 x[CPL][8];
+        uint4 gw[CPL][4];
+        if (wv == 0) {
+            const float* hv = hidden + static_cast<size_t>(min(t0, T - 1)) * D;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) x[j][q] = load_f4(hv + c * 32 + q * 4);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) gw[j][q] = load_u4(L.norm_w + c * 32 + q * 8);
+            }
+        }
+        if (rfirst < rend) {
+#pragma unroll
+            for (int ii = 0; ii < RG; ++ii) {
+                const uint16_t* wr = L.router_w + static_cast<size_t>(min(rfirst + ii, rend - 1)) * D;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const uint32_t c = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) rws[ii][j][q] = load_u4(wr + c * 32 + q * 8);
+                }
+            }
+        }
+        if (wv == 0) {
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const bool ok = lane + WAVE * j < nch;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    if (!ok) x[j][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    ss = fmaf(x[j][q].x, x[j][q].x, ss);
+                    ss = fmaf(x[j][q].y, x[j][q].y, ss);
+                    ss = fmaf(x[j][q].z, x[j][q].z, ss);
+                    ss = fmaf(x[j][q].w, x[j][q].w, ss);
+                }
+            }
+            ss = wave_sum(ss);
+            const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + 1e-6f);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const uint32_t g0 = (q & 1) ? gw[j][q >> 1].z : gw[j][q >> 1].x;
+                    const uint32_t g1 = (q & 1) ? gw[j][q >> 1].w : gw[j][q >> 1].y;
+                    a[0][j][4 * q + 0] = (x[j][q].x * inv) * bf16_to_f32(g0 & 0xFFFFu);
+                    a[0][j][4 * q + 1] = (x[j][q].y * inv) * bf16_to_f32(g0 >> 16);
+                    a[0][j][4 * q + 2] = (x[j][q].z * inv) * bf16_to_f32(g1 & 0xFFFFu);
+                    a[0][j][4 * q + 3] = (x[j][q].w * inv) * bf16_to_f32(g1 >> 16);
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    s_a[j][q][lane] = make_float4(a[0][j][4 * q], a[0][j][4 * q + 1], a[0][j][4 * q + 2],
+                                                  a[0][j][4 * q + 3]);
+            }
+            if (eg == 0 && t0 < T) {
+                float amax = 0.f;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j)
+                    if (lane + WAVE * j < nch) {
+#pragma unroll
+                        for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(a[0][j][k]));
+                    }
+                amax = wave_max(amax);
+                const int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
+                const size_t row = static_cast<size_t>(t0) * D;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    if (lane + WAVE * j >= nch) continue;
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const size_t o = row + (lane + WAVE * j) * 32 + 8 * b;
+                        uint4 hv4, lv4;
+                        split8_f16(&a[0][j][8 * b], e, hv4, lv4);
+                        *reinterpret_cast<uint4*>(x_hi + o) = hv4;
+                        *reinterpret_cast<uint4*>(x_lo + o) = lv4;
+                    }
+                }
+                if (lane == 0) x_sc[t0] = __builtin_ldexpf(1.0f, e);
+            }
+        }
+        __syncthreads();
+        if (wv != 0) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const float4 v = s_a[j][q][lane];
+                    a[0][j][4 * q] = v.x;
+                    a[0][j][4 * q + 1] = v.y;
+                    a[0][j][4 * q + 2] = v.z;
+                    a[0][j][4 * q + 3] = v.w;
+                }
+        }
+    } else
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
         const float* hv = hidden + static_cast<size_t>(min(t0 + t, T - 1)) * D;
+
         float4 x[CPL][8];
         uint4 g[CPL][4];
 #pragma unroll
@@ -182,15 +299,12 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
     // round trip per row: 21.4 us for the route at 512 tokens of the 30B
     // shape).  RG: as many rows as fit beside the normed activations
     // (TB * CPL * 32 values) in about 208 VGPRs, 16 CPL registers a row.
-    constexpr int RG_FIT = (208 - 32 * TB * CPL) / (16 * CPL);
-    constexpr int RG = RG_FIT >= RPB ? RPB : RG_FIT >= 8 ? 8 : RG_FIT >= 4 ? 4 : RG_FIT >= 2 ? 2 : 1;
-    static_assert(RPB % RG == 0, "row groups of a batch");
-    for (uint32_t r0 = rbeg + wv * RPB; r0 < rend; r0 += ROUTE_WAVES * RPB) {
+    // With ES > 1 the first group was requested before the norm (above).
+    for (uint32_t r0 = rfirst; r0 < rend; r0 += ROUTE_WAVES * RPB) {
         float part[RPB * TB];
-        uint4 rws[RG][CPL][4];
 #pragma unroll
         for (int i = 0; i < RPB; ++i) {
-            if (i % RG == 0) {
+            if (i % RG == 0 && (ES == 1 || i > 0 || r0 != rfirst)) {
 #pragma unroll
                 for (int ii = 0; ii < RG; ++ii) {
                     const uint16_t* wr = L.router_w + static_cast<size_t>(min(r0 + i + ii, rend - 1)) * D;
