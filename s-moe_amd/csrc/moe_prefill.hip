@@ -81,11 +81,12 @@ __device__ __forceinline__ void split8_f16(const float* x, int e, uint4& hi, uin
 // the blocks write their logits with agent-scope stores, wait for them, and
 // add themselves to a device-scope counter per token group; the block that
 // finds the count at ES - 1 modulo ES runs the group's top-k on agent-scope
-// loads of the logits (no device-wide fence anywhere).  There (one token a
-// block) only wave 0 reads and normalises the token and hands it to the other
-// waves through LDS, and every wave requests its first router rows before
-// that, so the hidden row's and the router rows' round trips overlap (at 64
-// tokens of the 235B shape 16.1 -> 13.3 us, same bits).
+// loads of the logits (no device-wide fence anywhere).  Where the registers
+// allow (HAND below), wave t alone reads and normalises token t and hands it
+// to the other waves through LDS, and every wave requests its first router
+// rows before that, so the hidden rows' and the router rows' round trips
+// overlap (same bits; 64 tokens of the 235B shape 16.1 -> 13.3 us, 512 of the
+// 30B shape 20.3 -> 18.1 us).
 // ---------------------------------------------------------------------------
 constexpr int ROUTE_WAVES = 8;
 
@@ -110,26 +111,30 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
     const uint32_t rows_per = (d.E + ES - 1) / ES, rbeg = eg * rows_per, rend = min(d.E, rbeg + rows_per);
     const uint32_t D = d.D, nch = D >> 5;
 
-    // router rows per load group (see below); with ES > 1 the wave's first
-    // group is requested before the norm
+    // router rows per load group (see below)
     constexpr int RG_FIT = (208 - 32 * TB * CPL) / (16 * CPL);
     constexpr int RG_ALL = RG_FIT >= RPB ? RPB : RG_FIT >= 8 ? 8 : RG_FIT >= 4 ? 4 : RG_FIT >= 2 ? 2 : 1;
-    // (two rows a group where wave 0's hidden chunks are live beside them)
-    constexpr int RG = ES > 1 && CPL > 1 && RG_ALL > 2 ? 2 : RG_ALL;
+    // HAND: waves 0 .. TB - 1 normalise the tokens and hand them over through
+    // LDS while every wave requests its first group of router rows (where that
+    // fits the registers without spills: one chunk a lane, or one token at two;
+    // E <= 128)
+    constexpr bool HAND = ES > 1 || (VPL == 2 && (CPL == 1 || (CPL == 2 && TB == 1)));
+    // (two rows a group where a wave's hidden chunks are live beside them)
+    constexpr int RG = HAND && CPL > 1 && RG_ALL > 2 ? 2 : RG_ALL;
     static_assert(RPB % RG == 0, "row groups of a batch");
     const uint32_t rfirst = rbeg + wv * RPB;
     uint4 rws[RG][CPL][4];
     float a[TB][CPL][32];
-    if constexpr (ES > 1) {
-        // one token: wave 0 normalises it (and, in the first block, writes its
-        // f16 planes) and hands it to the other waves through LDS; every wave
-        // requests its router rows before that, so the two round trips overlap
-        static_assert(TB == 1, "one token a block when the rows are split");
-        __shared__ __align__(16) float4 s_a[CPL][8][WAVE];
+    if constexpr (HAND) {
+        // wave t < TB normalises token t (and, in the token group's first
+        // block, writes its f16 planes) and hands it to the other waves
+        // through LDS; every wave requests its router rows before that, so the
+        // round trips overlap and each token is normalised once, not by every wave
+        __shared__ __align__(16) float4 s_a[TB][CPL][8][WAVE];
         float4 x[CPL][8];
         uint4 gw[CPL][4];
-        if (wv == 0) {
-            const float* hv = hidden + static_cast<size_t>(min(t0, T - 1)) * D;
+        if (wv < TB) {
+            const float* hv = hidden + static_cast<size_t>(min(t0 + wv, T - 1)) * D;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 const uint32_t c = min(lane + WAVE * j, nch - 1);
@@ -151,7 +156,7 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
                 }
             }
         }
-        if (wv == 0) {
+        if (wv < TB) {
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
@@ -180,10 +185,10 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
                 }
 #pragma unroll
                 for (int q = 0; q < 8; ++q)
-                    s_a[j][q][lane] = make_float4(a[0][j][4 * q], a[0][j][4 * q + 1], a[0][j][4 * q + 2],
-                                                  a[0][j][4 * q + 3]);
+                    s_a[wv][j][q][lane] = make_float4(a[0][j][4 * q], a[0][j][4 * q + 1], a[0][j][4 * q + 2],
+                                                      a[0][j][4 * q + 3]);
             }
-            if (eg == 0 && t0 < T) {
+            if (eg == 0 && t0 + wv < T) {
                 float amax = 0.f;
 #pragma unroll
                 for (int j = 0; j < CPL; ++j)
@@ -193,7 +198,7 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
                     }
                 amax = wave_max(amax);
                 const int e = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;
-                const size_t row = static_cast<size_t>(t0) * D;
+                const size_t row = static_cast<size_t>(t0 + wv) * D;
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
                     if (lane + WAVE * j >= nch) continue;
@@ -206,22 +211,22 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
                         *reinterpret_cast<uint4*>(x_lo + o) = lv4;
                     }
                 }
-                if (lane == 0) x_sc[t0] = __builtin_ldexpf(1.0f, e);
+                if (lane == 0) x_sc[t0 + wv] = __builtin_ldexpf(1.0f, e);
             }
         }
         __syncthreads();
-        if (wv != 0) {
+#pragma unroll
+        for (int t = 0; t < TB; ++t)
 #pragma unroll
             for (int j = 0; j < CPL; ++j)
 #pragma unroll
                 for (int q = 0; q < 8; ++q) {
-                    const float4 v = s_a[j][q][lane];
-                    a[0][j][4 * q] = v.x;
-                    a[0][j][4 * q + 1] = v.y;
-                    a[0][j][4 * q + 2] = v.z;
-                    a[0][j][4 * q + 3] = v.w;
+                    const float4 v = s_a[t][j][q][lane];
+                    a[t][j][4 * q] = v.x;
+                    a[t][j][4 * q + 1] = v.y;
+                    a[t][j][4 * q + 2] = v.z;
+                    a[t][j][4 * q + 3] = v.w;
                 }
-        }
     } else
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
@@ -304,7 +309,7 @@ void k_route(MoeDims d, LayerDesc L, const float* __restrict__ hidden, uint32_t 
         float part[RPB * TB];
 #pragma unroll
         for (int i = 0; i < RPB; ++i) {
-            if (i % RG == 0 && (ES == 1 || i > 0 || r0 != rfirst)) {
+            if (i % RG == 0 && (!HAND || i > 0 || r0 != rfirst)) {
 #pragma unroll
                 for (int ii = 0; ii < RG; ++ii) {
                     const uint16_t* wr = L.router_w + static_cast<size_t>(min(r0 + i + ii, rend - 1)) * D;
