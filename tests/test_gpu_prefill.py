@@ -296,3 +296,25 @@ def test_route_counters_across_launches(ctx, oracle):
             rid, rw = oracle.top_k(logits, layer.K, True)
             assert (gids[t] == rid).all(), (T, t)
             assert np.allclose(gw[t], rw, rtol=1e-5, atol=1e-7), (T, t)
+
+
+@pytest.mark.parametrize("D,E,K,I,T", [(4096, 128, 8, 256, 200), (2048, 16, 2, 128, 1100)])
+def test_route_block_shapes(ctx, oracle, D, E, K, I, T):
+    """Router block shapes beyond the benchmark configurations: one token a
+    block at d_model 4096 (128-511 tokens) and four tokens a block (1024 tokens
+    and more in one pass, possible where E*k is small), both with the tokens
+    normalised by one wave each and handed to the others through LDS.  Every
+    token's ids and weights against the oracle's router + top-k; the hidden
+    update of 32 tokens spread over the batch against an fp64 evaluation and
+    the oracle (check_against_oracle, exact=True: at d_model 4096 the oracle's
+    own fp32 rounding exceeds the plain 1e-3 bound, as in the 235B tests)."""
+    layer = Layer(ctx, D, E, K, I, layer_id=300 + D // 64 + T)
+    h0, got, gids, gw, _ = run_prefill(ctx, layer, T, index0=3000)
+    for t in range(T):
+        x = oracle.rms_norm_bf16(h0[t], layer.h_norm)
+        logits = oracle.matvec_bf16(layer.h_router.reshape(layer.E, layer.D), x)
+        rid, rw = oracle.top_k(logits, layer.K, True)
+        assert (gids[t] == rid).all(), t
+        assert np.allclose(gw[t], rw, rtol=1e-5, atol=1e-7), t
+    rows = np.linspace(0, T - 1, 32).astype(int)
+    assert check_against_oracle(oracle, layer, h0, got, gids, gw, rows=rows, exact=True) <= TOL
