@@ -134,7 +134,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the expert-parallel design for more GPUs is described in DESIGN.md)", file=sys.stderr)
+              "(over more GPUs the path would shard by expert: a dispatch of the normed tokens and a "
+              "combine of the weighted expert outputs per layer; not built here)", file=sys.stderr)
         sys.exit(2)
 
     import torch
