@@ -215,9 +215,33 @@ int smoe_hip_set_stream(SmoeMetalCtx* ctx, void* hip_stream);
 
 /* Synchronise the context's stream and report the device-side error flags
  * raised since the last call, then clear them: a timed-out routing exchange
- * inside smoe_hip_moe_decode (SMOE_ERR_HIP) or an expert id >= n_experts
- * given to smoe_hip_permute (SMOE_ERR_ARG). */
+ * inside smoe_hip_moe_decode / smoe_hip_moe_decode_stack (SMOE_ERR_HIP) or an
+ * expert id >= n_experts given to smoe_hip_permute (SMOE_ERR_ARG).  After a
+ * time-out every decode result since the previous call is suspect (waves of
+ * the failed launch may have published words tagged for later launches), so
+ * the call also clears the context's decode exchange words (epochs included)
+ * before it returns; the error itself only arises when a grid the host found
+ * co-resident is not. */
 int smoe_hip_synchronize(SmoeMetalCtx* ctx);
+
+/* Tags of the exchange words of the one-launch decode kernels (no
+ * counterpart in the reference; for tests and diagnostics).  For a launch of
+ * n_layers layers that reads `epoch` from its epoch word: tags[l] for layer l
+ * (tags may be NULL), the abort value of its bounded waits, and the epoch it
+ * leaves behind.  Tags lie in 1 .. 2^32 - 1 and wrap from 2^32 - 1 to 1, so
+ * no tag is 0 and no two consecutive layers (within a launch or across
+ * launches) share one. */
+void smoe_hip_exchange_tags(uint32_t epoch, uint32_t n_layers, uint32_t* tags, uint32_t* abort_val,
+                            uint32_t* next_epoch);
+
+/* Read (chain / layer non-NULL) or set (set_chain / set_layer non-NULL) the
+ * epoch word of the chained decode kernel's exchange words and of the
+ * one-launch layer kernel's (no counterpart in the reference; for tests that
+ * walk the tags across their wrap).  Synchronous, outside graph capture;
+ * SMOE_ERR_ARG if the words asked for are not allocated yet (they are after
+ * the first call of that kernel). */
+int smoe_hip_exchange_epoch(SmoeMetalCtx* ctx, const uint32_t* set_chain, const uint32_t* set_layer,
+                            uint32_t* chain, uint32_t* layer);
 
 /* Reserve device scratch for layers of this shape and up to max_tokens tokens
  * per call.  Entry points reserve on demand when the stream is not being
@@ -251,38 +275,22 @@ int smoe_hip_moe_decode(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
  *   SMOE_DECODE_LAUNCHES: exactly n_layers smoe_hip_moe_decode
  *     calls (one or two launches per layer, as that entry point chooses).
  *   SMOE_DECODE_SPLIT: the same calls, always two launches per layer.
- *   SMOE_DECODE_PERSISTENT: the whole step in one persistent kernel launch
- *     (no per-layer kernel boundary); results equal the per-layer calls up to
- *     fp32 summation order.  Its layer table is copied to the device when it
- *     differs from the previous call's (outside graph capture; under capture
- *     a new table gives SMOE_ERR_CAPTURE).  Shapes it does not cover
- *     (d_model > 2048, d_ff > 2048, more than 512 experts) take the launches.
- *   SMOE_DECODE_PREFETCH: one persistent launch per step as above, in which
- *     every CU copies its slice of the next layer's predicted experts (layer
- *     l + 1's router applied to layer l's input) into LDS while layer l runs;
- *     a mispredicted slice is fetched when the layer's exact top-k is known.
- *     The prediction changes only where weights come from, not results.
- *     Shapes: d_model 2048, top_k 8, 8..128 experts, d_ff a multiple of 192
- *     up to 768 (Qwen3-30B-A3B), on a device with 256 CUs; others take the
- *     launches.  Table handling as SMOE_DECODE_PERSISTENT.  Opt-in: at the
- *     30B shape it is currently slower per layer than SMOE_DECODE_LAUNCHES
- *     (copies in flight on a CU lengthen its exchange waits).
  *   SMOE_DECODE_CHAIN (default): the whole step in one launch that runs, layer after
  *     layer, the single-launch layer kernel's schedule (one top-k rank per
  *     XCD); every XCD combines all rows into its own copy of the next
  *     layer's input, so layer l + 1 starts inside the launch as soon as its
  *     XCD's copy is complete, with its router rows already requested.
- *     Shapes: those of the single-launch layer kernel whose registers allow
- *     a whole grid at once (Qwen3-30B-A3B); others take the launches.  Table
- *     handling as SMOE_DECODE_PERSISTENT. */
+ *     Results equal the per-layer calls bit for bit.  Shapes: those of the
+ *     single-launch layer kernel whose registers allow a whole grid at once
+ *     (both Qwen3 shapes); others take the launches.  Its layer table is
+ *     copied to the device when it differs from the previous call's (outside
+ *     graph capture; under capture a new table gives SMOE_ERR_CAPTURE). */
 int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* shape,
                               const SmoeMoeLayer* layers, uint32_t n_layers, float* hidden,
                               uint32_t* ids_out, float* weights_out);
 
 #define SMOE_DECODE_LAUNCHES   0
-#define SMOE_DECODE_PERSISTENT 1
 #define SMOE_DECODE_SPLIT      2
-#define SMOE_DECODE_PREFETCH   3
 #define SMOE_DECODE_CHAIN      4
 /* Select the engine of smoe_hip_moe_decode_stack (and, for SMOE_DECODE_SPLIT,
  * the form of smoe_hip_moe_decode) for this context. */
@@ -463,12 +471,10 @@ int smoe_hip_moe_decode_static(const SmoeMoeShape* shape, const SmoeMoeLayer* la
 #define SMOE_KERNEL_SCATTER       8   /* prefill: weighted combine of pair outputs + residual */
 #define SMOE_KERNEL_ROUTE         9   /* prefill: RMSNorm + router + top-k per token          */
 #define SMOE_KERNEL_SPLIT        10   /* prefill: f16 hi/lo planes of activations             */
-#define SMOE_KERNEL_STACK        11   /* decode: every layer of a stack in one launch         */
 #define SMOE_KERNEL_MOE_LAYER    12   /* decode: the whole MoE block of one token in one launch */
 #define SMOE_KERNEL_GEMV         13   /* dense trunk: grouped bf16 GEMV                          */
 #define SMOE_KERNEL_ATTENTION    14   /* dense trunk: QK norm/RoPE/KV append + decode attention   */
 #define SMOE_KERNEL_STREAM       15   /* measurement: streaming-read ceiling (smoe_hip_stream_read) */
-#define SMOE_KERNEL_STACK_PREFETCH 16 /* decode: every layer in one launch, predicted experts prefetched to LDS */
 #define SMOE_KERNEL_CHAIN        17 /* decode: every layer in one launch, the one-launch layer's schedule per layer */
 #define SMOE_KERNEL_KINDS        20
 int smoe_hip_profile_enable(SmoeMetalCtx* ctx, int enable);

@@ -61,12 +61,9 @@ struct PrefillScratch {
     float* y = nullptr;             // [P x D]
 };
 
-// persistent stack kernel: exchange words, control words, device layer table
-struct StackScratch {
-    size_t words = 0;               // capacity of xch
-    uint64_t* xch = nullptr;        // exchange words (zeroed once; the kernel keeps them)
-    uint32_t* ctl = nullptr;        // [ST_CTL_WORDS] control words (likewise)
-    LayerDesc* tbl = nullptr;       // [tbl_cap] device copy of the layer table
+// the chained decode kernel's device copy of the layer table
+struct LayerTable {
+    LayerDesc* tbl = nullptr;       // [tbl_cap]
     uint32_t tbl_cap = 0;
     std::vector<LayerDesc> host_tbl;   // what tbl holds
 };
@@ -108,7 +105,7 @@ struct SmoeMetalCtx {
 
     DeviceScratch ds;
     PrefillScratch ps;
-    StackScratch ss;
+    LayerTable lt;
     ChainScratch cs;
     int decode_engine = SMOE_DECODE_CHAIN;      // smoe_hip_moe_decode_stack's engine
     uint32_t* d_err = nullptr;       // [1] device-side error flags (bit 0: exchange time-out, bit 1: bad expert id)
@@ -422,9 +419,7 @@ extern "C" void smoe_metal_destroy(SmoeMetalCtx* ctx)
     if (ctx->own_stream && ctx->own_stream != ctx->stream) (void)hipStreamSynchronize(ctx->own_stream);
     free_device_scratch(ctx->ds);
     free_prefill_scratch(ctx->ps);
-    dfree(ctx->ss.xch);
-    dfree(ctx->ss.ctl);
-    dfree(ctx->ss.tbl);
+    dfree(ctx->lt.tbl);
     dfree(ctx->cs.xch);
     dfree(ctx->cs.hcopy);
     dfree(ctx->cs.cnt);
@@ -723,6 +718,23 @@ extern "C" int smoe_hip_set_stream(SmoeMetalCtx* ctx, void* hip_stream)
     return SMOE_OK;
 }
 
+// every decode exchange word of the context back to zero (epochs included),
+// synchronously; the stream must be idle
+static int rearm_exchange(SmoeMetalCtx* ctx)
+{
+    DeviceScratch& s = ctx->ds;
+    ChainScratch& c = ctx->cs;
+    if (s.ll && !hip_ok(ctx, hipMemset(s.ll, 0, size_t(s.T) * smoe::ll_token_words(s.E) * sizeof(uint64_t)),
+                        "hipMemset(ll)"))
+        return SMOE_ERR_HIP;
+    if (s.lx && !hip_ok(ctx, hipMemset(s.lx, 0, smoe::lx_words(s.D, s.E, s.I) * sizeof(uint64_t)), "hipMemset(lx)"))
+        return SMOE_ERR_HIP;
+    if (c.xch && !hip_ok(ctx, hipMemset(c.xch, 0, c.words * sizeof(uint64_t)), "hipMemset(chain xch)")) return SMOE_ERR_HIP;
+    if (c.cnt && !hip_ok(ctx, hipMemset(c.cnt, 0, smoe::chain_cnt_words() * sizeof(uint32_t)), "hipMemset(chain cnt)"))
+        return SMOE_ERR_HIP;
+    return hip_ok(ctx, hipDeviceSynchronize(), "hipDeviceSynchronize") ? SMOE_OK : SMOE_ERR_HIP;
+}
+
 extern "C" int smoe_hip_synchronize(SmoeMetalCtx* ctx)
 {
     if (!ctx) return SMOE_ERR_ARG;
@@ -734,12 +746,51 @@ extern "C" int smoe_hip_synchronize(SmoeMetalCtx* ctx)
         if (e) {
             // reported once: clear for the next call
             if (!hip_ok(ctx, hipMemset(ctx->d_err, 0, sizeof(uint32_t)), "hipMemset(err)")) return SMOE_ERR_HIP;
+            // After a time-out, waves of the failed launch that started late
+            // may have left exchange words tagged for the launches after it:
+            // every result since the previous synchronize is suspect, and the
+            // exchange words start again from zero.
+            if ((e & 1u) && rearm_exchange(ctx) != SMOE_OK) return SMOE_ERR_HIP;
             std::snprintf(ctx->last_err, sizeof(ctx->last_err), "device:%s%s%s (flags %u)",
                           (e & 1u) ? " routing exchange timed out" : "", (e & 2u) ? " expert id out of range" : "",
                           (e & 4u) ? " a stack block ran off its XCD (later calls write exchange words through)"
                                    : "",
                           e);
             return (e & 5u) ? SMOE_ERR_HIP : SMOE_ERR_ARG;
+        }
+    }
+    return SMOE_OK;
+}
+
+extern "C" void smoe_hip_exchange_tags(uint32_t epoch, uint32_t n_layers, uint32_t* tags, uint32_t* abort_val,
+                                       uint32_t* next_epoch)
+{
+    for (uint32_t l = 0; tags && l < n_layers; ++l) tags[l] = smoe::tag_at(epoch, l);
+    if (abort_val) *abort_val = smoe::tag_at(epoch, 0);
+    if (next_epoch) *next_epoch = smoe::epoch_after(epoch, n_layers);
+}
+
+extern "C" int smoe_hip_exchange_epoch(SmoeMetalCtx* ctx, const uint32_t* set_chain, const uint32_t* set_layer,
+                                       uint32_t* chain, uint32_t* layer)
+{
+    if (!ctx) return SMOE_ERR_ARG;
+    if (stream_capturing(ctx->stream)) return SMOE_ERR_CAPTURE;
+    uint64_t* words[2] = {ctx->cs.xch, ctx->ds.lx};
+    const uint32_t* set[2] = {set_chain, set_layer};
+    uint32_t* get[2] = {chain, layer};
+    if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
+    for (int i = 0; i < 2; ++i) {
+        if ((set[i] || get[i]) && !words[i]) return SMOE_ERR_ARG;
+        if (set[i]) {
+            const uint64_t v = *set[i];
+            if (!hip_ok(ctx, hipMemcpy(words[i], &v, sizeof(v), hipMemcpyHostToDevice), "hipMemcpy(epoch)"))
+                return SMOE_ERR_HIP;
+        }
+        if (get[i]) {
+            uint64_t v = 0;
+            if (!hip_ok(ctx, hipMemcpy(&v, words[i], sizeof(v), hipMemcpyDeviceToHost), "hipMemcpy(epoch)"))
+                return SMOE_ERR_HIP;
+            *get[i] = static_cast<uint32_t>(v);
         }
     }
     return SMOE_OK;
@@ -756,8 +807,7 @@ extern "C" int smoe_hip_stream_read(SmoeMetalCtx* ctx, const void* src, uint64_t
 
 extern "C" int smoe_hip_set_decode_engine(SmoeMetalCtx* ctx, int engine)
 {
-    if (!ctx || (engine != SMOE_DECODE_LAUNCHES && engine != SMOE_DECODE_PERSISTENT && engine != SMOE_DECODE_SPLIT &&
-                 engine != SMOE_DECODE_PREFETCH && engine != SMOE_DECODE_CHAIN))
+    if (!ctx || (engine != SMOE_DECODE_LAUNCHES && engine != SMOE_DECODE_SPLIT && engine != SMOE_DECODE_CHAIN))
         return SMOE_ERR_ARG;
     ctx->decode_engine = engine;
     return SMOE_OK;
@@ -819,7 +869,7 @@ static bool same_layer(const LayerDesc& a, const LayerDesc& b)
 // capture: under capture a new table gives SMOE_ERR_CAPTURE)
 static int upload_table(SmoeMetalCtx* ctx, const SmoeMoeLayer* layers, uint32_t n_layers)
 {
-    StackScratch& s = ctx->ss;
+    LayerTable& s = ctx->lt;
     bool same = s.tbl && s.host_tbl.size() == n_layers;
     for (uint32_t l = 0; same && l < n_layers; ++l) same = same_layer(s.host_tbl[l], layer_of(&layers[l]));
     if (same) return SMOE_OK;
@@ -880,7 +930,7 @@ static int decode_chain(SmoeMetalCtx* ctx, const MoeDims& d, const SmoeMoeLayer*
     const int rc = upload_table(ctx, layers, n_layers);
     if (rc != SMOE_OK) return rc;
     if (!timed(ctx, SMOE_KERNEL_CHAIN, "moe_chain", [&] {
-            return smoe::launch_moe_chain(d, ctx->ss.tbl, n_layers, hidden, c.xch, c.hcopy, c.cnt,
+            return smoe::launch_moe_chain(d, ctx->lt.tbl, n_layers, hidden, c.xch, c.hcopy, c.cnt,
                                           ids_out ? ids_out : c.ids, weights_out ? weights_out : c.w, ctx->d_err,
                                           ctx->stream);
         }))
@@ -904,57 +954,12 @@ extern "C" int smoe_hip_moe_decode_stack(SmoeMetalCtx* ctx, const SmoeMoeShape* 
         if (smoe::chain_supported(d, host.data(), n_layers))
             return decode_chain(ctx, d, layers, n_layers, hidden, ids_out, weights_out);
     }
-    const bool spec = ctx->decode_engine == SMOE_DECODE_PREFETCH && smoe::spec_supported(d);
-    if (!spec && (ctx->decode_engine != SMOE_DECODE_PERSISTENT || !smoe::stack_supported(d))) {
-        // two launches per layer
-        for (uint32_t l = 0; l < n_layers; ++l) {
-            rc = moe_forward(ctx, shape, &layers[l], hidden, 1, ids_out ? ids_out + size_t(l) * d.K : nullptr,
-                             weights_out ? weights_out + size_t(l) * d.K : nullptr);
-            if (rc != SMOE_OK) return rc;
-        }
-        return SMOE_OK;
+    // one or two launches per layer
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        rc = moe_forward(ctx, shape, &layers[l], hidden, 1, ids_out ? ids_out + size_t(l) * d.K : nullptr,
+                         weights_out ? weights_out + size_t(l) * d.K : nullptr);
+        if (rc != SMOE_OK) return rc;
     }
-    StackScratch& s = ctx->ss;
-    const bool capturing = stream_capturing(ctx->stream);
-    // exchange words: grown (and zeroed) outside capture only
-    const uint32_t nl = std::min<uint32_t>(n_layers, smoe::ST_MAX_LAYERS);
-    const size_t words = spec ? smoe::spec_xch_words(d, nl) : smoe::stack_xch_words(d, nl);
-    if (!s.ctl || s.words < words) {
-        if (capturing) return SMOE_ERR_CAPTURE;
-        if (!hip_ok(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return SMOE_ERR_HIP;
-        dfree(s.xch);
-        s.words = 0;
-        if (!s.ctl) {
-            if (!dalloc(ctx, &s.ctl, smoe::ST_CTL_WORDS) ||
-                !hip_ok(ctx, hipMemset(s.ctl, 0, smoe::ST_CTL_WORDS * sizeof(uint32_t)), "hipMemset(ctl)"))
-                return SMOE_ERR_HIP;
-        }
-        // flags only ever grow (the control word keeps the epoch), so fresh
-        // zeroed words can never match a live flag
-        if (!dalloc(ctx, &s.xch, words) ||
-            !hip_ok(ctx, hipMemset(s.xch, 0, words * sizeof(uint64_t)), "hipMemset(xch)"))
-            return SMOE_ERR_HIP;
-        s.words = words;
-    }
-    // device layer table: uploaded when it changes (outside capture)
-    rc = upload_table(ctx, layers, n_layers);
-    if (rc != SMOE_OK) return rc;
-    // one launch per ST_MAX_LAYERS layers (the kernel keeps its layer table in LDS)
-    for (uint32_t l0 = 0; l0 < n_layers; l0 += smoe::ST_MAX_LAYERS) {
-        const uint32_t n = std::min<uint32_t>(smoe::ST_MAX_LAYERS, n_layers - l0);
-        uint32_t* ids = ids_out ? ids_out + size_t(l0) * d.K : nullptr;
-        float* w = weights_out ? weights_out + size_t(l0) * d.K : nullptr;
-        const bool ok = spec ? timed(ctx, SMOE_KERNEL_STACK_PREFETCH, "decode_spec", [&] {
-                                   return smoe::launch_decode_spec(d, s.tbl + l0, n, hidden, s.xch, s.ctl, ids, w,
-                                                                   ctx->d_err, nullptr, ctx->stream);
-                               })
-                             : timed(ctx, SMOE_KERNEL_STACK, "decode_stack", [&] {
-                                   return smoe::launch_decode_stack(d, s.tbl + l0, n, hidden, s.xch, s.ctl, ids, w,
-                                                                    ctx->d_err, ctx->stream);
-                               });
-        if (!ok) return SMOE_ERR_HIP;
-    }
-    ctx->dispatches.fetch_add(uint64_t(n_layers) * d.K, std::memory_order_relaxed);
     return SMOE_OK;
 }
 

@@ -88,10 +88,34 @@ hipError_t launch_gate_up(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n_ex
 hipError_t launch_down_combine(const MoeDims& d, const ExpertPtrs* tbl, const float* h, const float* w,
                                float* hidden, uint64_t* ll, uint32_t n_tok, hipStream_t s);
 // ---- decode, one token, one launch (moe_layer.hip) -----------------------
-// Exchange words of the one-launch layer: word 0 holds the epoch (the tag of
-// the last launch), then 8 logit copies of lx_pad(E) words, 8 h copies of
-// lx_pad(I) words and 8 rank partials of lx_pad(D) words.  Zero once at
-// allocation; never re-armed.
+// Exchange-word tags of the one-launch decode kernels.  The epoch word holds
+// a count e in [0, TAG_PERIOD); the words of layer l of a launch that read e
+// carry tag_at(e, l) = ((e + l) mod TAG_PERIOD) + 1, and the launch leaves
+// epoch_after(e, n_layers) behind.  Tags therefore run through 1 .. 2^32 - 1
+// and wrap from 2^32 - 1 to 1: never 0 (every word's value at allocation),
+// and two consecutive layers, in one launch or across launches, never share
+// one.  Any 32-bit value read from the word is reduced first, so a word
+// holding 2^32 - 1 counts as 0.
+constexpr uint32_t TAG_PERIOD = 0xFFFFFFFFu;
+__host__ __device__ constexpr uint32_t tag_mod(uint64_t s)
+{
+    // s mod (2^32 - 1): 2^32 is 1 modulo the period, so fold the high word in
+    const uint64_t f = (s & 0xFFFFFFFFull) + (s >> 32);   // < 2^33
+    const uint64_t g = (f & 0xFFFFFFFFull) + (f >> 32);   // <= 2^32
+    return static_cast<uint32_t>(g >= TAG_PERIOD ? g - TAG_PERIOD : g);
+}
+__host__ __device__ constexpr uint32_t tag_at(uint32_t epoch, uint32_t l)
+{
+    return tag_mod(static_cast<uint64_t>(epoch) + l) + 1u;
+}
+__host__ __device__ constexpr uint32_t epoch_after(uint32_t epoch, uint32_t n_layers)
+{
+    return tag_mod(static_cast<uint64_t>(epoch) + n_layers);
+}
+// Exchange words of the one-launch layer: word 0 holds the epoch (above),
+// then 8 logit copies of lx_pad(E) words, 8 h copies of lx_pad(I) words and
+// 8 rank partials of lx_pad(D) words.  Zero once at allocation; never
+// re-armed (a launch that times out leaves them to be cleared by the host).
 constexpr uint32_t LX_HEAD = 64;
 constexpr uint32_t LX_MAX_I = 2048;
 __host__ __device__ constexpr uint32_t lx_pad(uint32_t n) { return ((n + 63u) & ~63u) + 64u; }
@@ -136,36 +160,6 @@ hipError_t launch_down_slots(const MoeDims& d, const ExpertPtrs* tbl, uint32_t n
 hipError_t launch_topk(const float* scores, uint32_t rows, uint32_t n, uint32_t k,
                        uint32_t norm, uint32_t* ids, float* w, hipStream_t s);
 
-
-// ---- decode, whole stack in one persistent launch (moe_stack.hip) ---------
-// 256 blocks of 4 waves, one per CU of MI355X (8 XCDs x 32 CUs).
-constexpr int ST_BLOCKS = 256;
-constexpr int ST_WPB = 4;
-constexpr int ST_THREADS = ST_WPB * 64;
-constexpr uint32_t ST_WX = ST_BLOCKS / 8 * ST_WPB;   // waves per XCD
-constexpr uint32_t ST_CTL_WORDS = 352;               // control words (11 lines of 128 B)
-constexpr uint32_t ST_MAX_LAYERS = 128;              // layers per launch (the table sits in LDS)
-bool stack_supported(const MoeDims& d);
-// exchange words (uint64) the stack kernel needs for n_layers layers
-size_t stack_xch_words(const MoeDims& d, uint32_t n_layers);
-// hidden [D] += MoE_l(RMSNorm(hidden)) for l = 0 .. n_layers-1 (layers: device
-// array, n_layers <= ST_MAX_LAYERS); ids/w [n_layers x K] optional.  xch zeroed once at allocation, ctl
-// [ST_CTL_WORDS] likewise; both are kept by the kernel between calls.
-hipError_t launch_decode_stack(const MoeDims& d, const LayerDesc* layers, uint32_t n_layers, float* hidden,
-                               uint64_t* xch, uint32_t* ctl, uint32_t* ids, float* w, uint32_t* err, hipStream_t s);
-
-// ---- decode, whole stack in one persistent launch with LDS prefetch of the
-// predicted experts (moe_spec.hip) ---------------------------------------------
-// d_model 2048, top-k 8, n_experts 8..128, d_ff a multiple of 192 up to 768;
-// 256 blocks of 12 waves, one per CU (the device must have exactly 256 CUs).
-bool spec_supported(const MoeDims& d);
-size_t spec_xch_words(const MoeDims& d, uint32_t n_layers);
-// as launch_decode_stack; trace (optional) receives 16 words per (layer,
-// block): phase timestamps of compute wave 0 (s_memrealtime) and, in word 15,
-// hits << 32 | hit << 16 | slot expert
-hipError_t launch_decode_spec(const MoeDims& d, const LayerDesc* layers, uint32_t n_layers, float* hidden,
-                              uint64_t* xch, uint32_t* ctl, uint32_t* ids, float* w, uint32_t* err, uint64_t* trace,
-                              hipStream_t s);
 
 // out [rows] = W [rows x cols] bf16 . x [cols] (reference-surface dense GEMV)
 hipError_t launch_matvec_bf16(const uint16_t* W, const float* x, float* out, uint32_t rows, uint32_t cols,

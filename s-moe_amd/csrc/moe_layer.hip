@@ -679,8 +679,8 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
     const uint32_t nbx = (gridDim.x >> 3) * NW;
     const uint32_t t = (blockIdx.x >> 3) * NW + (NW > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0u);
     const uint32_t x = xcc_id();
-    uint32_t tag = static_cast<uint32_t>(get_agent(lx)) + 1u;
-    tag = __builtin_amdgcn_readfirstlane(tag ? tag : 1u);
+    const uint32_t ep = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(get_agent(lx)));
+    const uint32_t tag = tag_at(ep, 0);
     LayerIO io{};
     io.hin = hidden;
     io.hout = hidden;
@@ -690,7 +690,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
     // the combiner of row block 0 on XCD 0 advances the epoch
     if (x == 0 && t == 0 && t < n_down) {
         __builtin_amdgcn_wave_barrier();
-        if ((threadIdx.x & (WAVE - 1)) == 0) put_agent(lx, static_cast<uint64_t>(tag));
+        if ((threadIdx.x & (WAVE - 1)) == 0) put_agent(lx, static_cast<uint64_t>(epoch_after(ep, 1)));
     }
     if (to) atomicOr(err, 1u);
 }
@@ -700,7 +700,9 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
 // of the next layer's input (in its L2; one flag per row block, carrying the
 // layer's tag, says when it is complete) and the last layer combining into
 // `hidden` on XCD 0.  The flags and the copy are only ever read by the XCD
-// that wrote them, after the flags, past the CU's L1.  Tags: epoch + l + 1 for layer l; the rank partials
+// that wrote them, after the flags, past the CU's L1.  Tags: tag_at(epoch, l)
+// for layer l (never 0, and never the same for two consecutive layers, in
+// one launch or across launches, whatever the epoch); the rank partials
 // alternate between two sets of words by layer parity (an XCD can start
 // layer l + 1's partials while another XCD still reads layer l's, never layer
 // l - 1's: that needs every XCD's layer l partials).  A wave that times out
@@ -726,9 +728,7 @@ void k_moe_chain(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_lay
         const LayerDesc L = layers[l];
         const bool last = l + 1 == n_layers;
         LayerIO io{};
-        uint32_t tag = ep0 + l + 1u, prev = ep0 + l;
-        tag = tag ? tag : 1u;
-        prev = prev ? prev : 1u;
+        const uint32_t tag = tag_at(ep0, l), prev = tag_at(ep0, l - 1u);   // (prev: l > 0 only)
         io.hin = l == 0 ? hidden : hx;
         io.wait = l > 0 ? flags_x : nullptr;
         io.wait_tag = prev;
@@ -737,7 +737,7 @@ void k_moe_chain(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_lay
         io.flag = last ? nullptr : flags_x;
         io.py = py0 + (l & 1u) * 8u * lx_pad(d.D);
         io.abort = cnt + 8 * CHAIN_FLAGS;
-        io.abort_val = ep0 + 1u;
+        io.abort_val = tag_at(ep0, 0);
         io.next_router = last ? nullptr : layers[l + 1].router_w;
         to |= moe_layer_step<CPL, VPL, SEG, DR, RB, NW, true>(d, L, io, lx, tag, ids_out + l * d.K,
                                                                w_out + l * d.K, n_up, n_down, t, x, nbx);
@@ -746,7 +746,7 @@ void k_moe_chain(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_lay
     // needs every wave's last partials)
     if (x == 0 && t == 0) {
         __builtin_amdgcn_wave_barrier();
-        if ((threadIdx.x & (WAVE - 1)) == 0) put_agent(lx, static_cast<uint64_t>(ep0 + n_layers));
+        if ((threadIdx.x & (WAVE - 1)) == 0) put_agent(lx, static_cast<uint64_t>(epoch_after(ep0, n_layers)));
     }
     if (to) atomicOr(err, 1u);
 }
@@ -981,8 +981,10 @@ static bool deal_known_round_robin()
 static bool layer_aligned(const LayerDesc& L)
 {
     // 16-byte pieces of every tensor (the reference's blobs place tensors
-    // back to back with sizes that are multiples of 16)
-    bool aligned = reinterpret_cast<uintptr_t>(L.experts) % 16 == 0 && L.stride % 16 == 0;
+    // back to back with sizes that are multiples of 16), the norm weights and
+    // router rows included (both read with 16-byte loads)
+    bool aligned = reinterpret_cast<uintptr_t>(L.experts) % 16 == 0 && L.stride % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(L.norm_w) % 16 == 0 && reinterpret_cast<uintptr_t>(L.router_w) % 16 == 0;
     for (int i = 0; i < 6; ++i) aligned = aligned && L.off[i] % 16 == 0;
     return aligned;
 }

@@ -102,6 +102,8 @@ SIGNATURES = [
     ("smoe_metal_attention_layer", None, [_VP, C.POINTER(SmoeAttnLayerArgs)]),
     ("smoe_hip_set_stream", _I, [_VP, _VP]),
     ("smoe_hip_synchronize", _I, [_VP]),
+    ("smoe_hip_exchange_tags", None, [_U32, _U32, _VP, _VP, _VP]),
+    ("smoe_hip_exchange_epoch", _I, [_VP, _VP, _VP, _VP, _VP]),
     ("smoe_hip_reserve", _I, [_VP, _SHP, _U32]),
     ("smoe_hip_moe_decode", _I, [_VP, _SHP, _LAY, _VP, _U32, _VP, _VP]),
     ("smoe_hip_moe_decode_stack", _I, [_VP, _SHP, _LAY, _U32, _VP, _VP, _VP]),
@@ -135,13 +137,13 @@ SIGNATURES = [
 
 KERNEL_MOE_UP, KERNEL_GATE_UP, KERNEL_MOE_DOWN, KERNEL_DOWN_SLOTS, KERNEL_TOPK = 0, 1, 2, 3, 4
 KERNEL_PERMUTE, KERNEL_GROUPED_GATE_UP, KERNEL_GROUPED_DOWN, KERNEL_SCATTER = 5, 6, 7, 8
-KERNEL_ROUTE, KERNEL_SPLIT, KERNEL_STACK, KERNEL_MOE_LAYER = 9, 10, 11, 12
-KERNEL_GEMV, KERNEL_ATTENTION, KERNEL_STREAM, KERNEL_STACK_PREFETCH, KERNEL_CHAIN = 13, 14, 15, 16, 17
-DECODE_LAUNCHES, DECODE_PERSISTENT, DECODE_SPLIT, DECODE_PREFETCH, DECODE_CHAIN = 0, 1, 2, 3, 4
+KERNEL_ROUTE, KERNEL_SPLIT, KERNEL_MOE_LAYER = 9, 10, 12
+KERNEL_GEMV, KERNEL_ATTENTION, KERNEL_STREAM, KERNEL_CHAIN = 13, 14, 15, 17
+DECODE_LAUNCHES, DECODE_SPLIT, DECODE_CHAIN = 0, 2, 4
 KERNEL_NAMES = {0: "moe_up", 1: "gate_up", 2: "moe_down", 3: "down_slots", 4: "topk",
                 5: "permute", 6: "grouped_gate_up", 7: "grouped_down", 8: "combine", 9: "route",
-                10: "split", 11: "decode_stack", 12: "moe_layer", 13: "gemv", 14: "attention",
-                15: "stream_read", 16: "decode_spec", 17: "moe_chain"}
+                10: "split", 12: "moe_layer", 13: "gemv", 14: "attention",
+                15: "stream_read", 17: "moe_chain"}
 
 _lib = None
 
@@ -258,9 +260,29 @@ class Context:
             self._check(self.lib.smoe_hip_attention_layer(self.ptr, C.byref(args)), "attention_layer")
 
     def set_decode_engine(self, engine: int):
-        """DECODE_LAUNCHES (per-layer calls), DECODE_PERSISTENT (one launch per step) or
-        DECODE_SPLIT (per-layer calls, always two launches per layer)."""
+        """DECODE_CHAIN (one launch per step, the default), DECODE_LAUNCHES (per-layer
+        calls) or DECODE_SPLIT (per-layer calls, always two launches per layer)."""
         self._check(self.lib.smoe_hip_set_decode_engine(self.ptr, engine), "set_decode_engine")
+
+    def exchange_epoch(self, set_chain=None, set_layer=None):
+        """smoe_hip_exchange_epoch: optionally set the chained kernel's and the
+        one-launch layer kernel's epoch words; returns (chain, layer) as read
+        afterwards (None for words not allocated yet)."""
+        out = []
+        for i, v in enumerate((set_chain, set_layer)):
+            val = C.c_uint32(v or 0)
+            got = C.c_uint32(0)
+            args = [None, None, None, None]
+            if v is not None:
+                args[i] = C.byref(val)
+            args[2 + i] = C.byref(got)
+            rc = self.lib.smoe_hip_exchange_epoch(self.ptr, *args)
+            if rc == SMOE_ERR_ARG and v is None:
+                out.append(None)
+                continue
+            self._check(rc, "exchange_epoch")
+            out.append(got.value)
+        return tuple(out)
 
     def moe_decode_stack(self, shape, layers, hidden: int, ids: int = 0, weights: int = 0):
         """layers: a sequence of SmoeMoeLayer (or a ctypes array of them)."""
@@ -381,3 +403,12 @@ class Vault:
 
     def load(self, dev_pool: int, pool_bytes: int, stream: int | None = None):
         self._check(self.lib.smoe_hip_vault_load(self.ptr, dev_pool, pool_bytes, stream or None), "vault_load")
+
+
+def exchange_tags(epoch: int, n_layers: int):
+    """smoe_hip_exchange_tags (host only): (tags [n_layers], abort value, next
+    epoch) of a one-launch decode of n_layers layers that reads `epoch`."""
+    tags = (C.c_uint32 * max(n_layers, 1))()
+    ab, nxt = C.c_uint32(0), C.c_uint32(0)
+    lib().smoe_hip_exchange_tags(epoch, n_layers, tags, C.byref(ab), C.byref(nxt))
+    return [int(t) for t in tags[:n_layers]], ab.value, nxt.value

@@ -1,0 +1,259 @@
+"""The decode stack at the configs' own depth (BASELINE configs 2 and 3), and
+the chained kernel's exchange tags across their 32-bit wrap.
+
+- Config 2: 48 Qwen3-30B-A3B-shaped layers, 256 consecutive decode steps,
+  each step's output feeding the next (the decode.cpp:121 layer loop run once
+  per token).  The chained launch (the bench's timed engine) must equal the
+  per-layer launches bit for bit over all 256 steps; at four of the steps
+  every layer is checked against the CPU oracle on the GPU's own input of
+  that layer (ids bit-exact, MoE delta within 1e-3); and the free-running
+  oracle is followed end to end until its first top-k disagreement, where
+  the oracle on the GPU's own input of that layer must agree with the GPU
+  (the inputs drifted apart; the layer itself is exact).
+- Config 3: 94 Qwen3-235B-A22B-shaped layers on one ~120 GB device pool:
+  one chained step equal to the per-layer launches bit for bit, layers 0, 47
+  and 93 checked against the oracle.
+- The wrap: the chain's epoch word seeded just below 2^32 - 1, so a 48-layer
+  launch runs its tags across the wrap, must still equal the per-layer
+  launches bit for bit, twice in a row, and leave the epoch the tag
+  arithmetic says.
+"""
+import numpy as np
+import pytest
+import torch
+
+import smoe_amd
+from gpu_helpers import SEED, moe_delta_err, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+M = 2**32 - 1
+
+
+class Stack:
+    """n_layers layers of one shape in one device pool, as the bench builds
+    them (layer l's experts, router and norm weights from the generator)."""
+
+    def __init__(self, ctx, D, E, K, I, n_layers, first_layer=0):
+        self.D, self.E, self.K, self.I, self.n = D, E, K, I, n_layers
+        self.shape = smoe_amd.make_shape(D, E, K, I)
+        self.off, self.raw, self.stride = smoe_amd.blob_layout(D, I)
+        lb = E * self.stride
+        self.lb = lb
+        torch.cuda.empty_cache()
+        self.pool = torch.empty(n_layers * lb, dtype=torch.uint8, device="cuda")
+        for l0 in range(0, n_layers, 8):
+            m = min(8, n_layers - l0)
+            ctx.synth_expert_pool(self.pool.data_ptr() + l0 * lb, first_layer + l0, m, E, self.stride,
+                                  self.shape, SEED, 0.02)
+            torch.cuda.synchronize()
+        self.router = torch.empty((n_layers, E * D), dtype=torch.int16, device="cuda")
+        for l in range(n_layers):
+            ctx.synth_bf16(self.router[l].data_ptr(), E * D, SEED, smoe_amd.router_stream(first_layer + l), 0.02)
+        self.norm_w = torch.full((D,), 0x3F80, dtype=torch.int16, device="cuda")
+        self.layers = [smoe_amd.make_layer(self.norm_w.data_ptr(), self.router[l].data_ptr(),
+                                           self.pool.data_ptr() + l * lb, self.stride, self.off)
+                       for l in range(n_layers)]
+        self.arr = (smoe_amd.SmoeMoeLayer * n_layers)(*self.layers)
+        torch.cuda.synchronize()
+        self._host = {}
+
+    def oshape(self):
+        return dict(d_model=self.D, n_experts=self.E, top_k=self.K, d_ff=self.I, group_size=64, norm_topk=1)
+
+    def host(self, l):
+        """Host copies of layer l's weights for the oracle (cached)."""
+        if l not in self._host:
+            self._host[l] = (self.norm_w.cpu().numpy().view(np.uint16), self.router[l].cpu().numpy().view(np.uint16),
+                             self.pool[l * self.lb:(l + 1) * self.lb].cpu().numpy())
+        return self._host[l]
+
+    def oracle(self, O, l, h):
+        nw, rw, pool = self.host(l)
+        return O.moe_decode_layer(self.oshape(), nw, rw, pool, self.stride, self.off, h)
+
+    def chain_step(self, ctx, hid, ids, w):
+        ctx.set_decode_engine(smoe_amd.DECODE_CHAIN)
+        ctx.moe_decode_stack(self.shape, self.arr, hid.data_ptr(), ids.data_ptr(), w.data_ptr())
+
+    def layer_step(self, ctx, hid, ids, w, inputs=None):
+        """The per-layer launches (one smoe_hip_moe_decode per layer);
+        inputs, when given, receives a copy of every layer's input."""
+        for l in range(self.n):
+            if inputs is not None:
+                inputs[l].copy_(hid)
+            ctx.moe_decode(self.shape, self.layers[l], hid.data_ptr(), 1, ids[l].data_ptr(), w[l].data_ptr())
+
+
+def margin_8_9(logits, k=8):
+    """The oracle's probability gap between ranks k and k+1, relative to p_k."""
+    z = np.asarray(logits, np.float64)
+    p = np.exp(z - z.max())
+    p /= p.sum()
+    s = np.sort(p)[::-1]
+    return float((s[k - 1] - s[k]) / s[k - 1])
+
+
+def check_layer(st, O, l, h_in, h_out, gids, gw):
+    out, oid, ow, logits, normed, yo = st.oracle(O, l, h_in)
+    assert (gids == oid).all(), (l, gids, oid)
+    assert np.allclose(gw, ow, rtol=1e-5, atol=1e-7)
+    e1, _ = moe_delta_err(h_out, h_in, yo, ow)
+    e2, _ = rel_err(h_out, out)
+    return max(e1, e2)
+
+
+@pytest.fixture(scope="module")
+def stack30(ctx):
+    st = Stack(ctx, 2048, 128, 8, 768, 48)
+    yield st
+    st.pool = None
+    torch.cuda.empty_cache()
+
+
+def test_config2_48_layers_256_steps(ctx, oracle, stack30):
+    """Config 2 at its workload: 256 chained steps equal 256 x 48 per-layer
+    launches bit for bit (hidden after every step, ids and weights of every
+    layer); steps 0, 1, 128 and 255 teacher-forced against the oracle layer by
+    layer; the free-running oracle followed until its first disagreement."""
+    O = oracle
+    st = stack30
+    D, K, NL, STEPS = st.D, st.K, st.n, 256
+    check_steps = (0, 1, 128, 255)
+    x0 = torch.empty(D, dtype=torch.float32, device="cuda")
+    ctx.synth_normal(x0.data_ptr(), D, SEED, smoe_amd.hidden_stream(0), 1.0)
+    a, b = x0.clone(), x0.clone()
+    ia = torch.zeros((NL, K), dtype=torch.int32, device="cuda")
+    wa = torch.zeros((NL, K), dtype=torch.float32, device="cuda")
+    ib, wb = torch.zeros_like(ia), torch.zeros_like(wa)
+    E2E = 16                                   # steps followed end to end
+    hist = torch.zeros((E2E, NL, D), dtype=torch.float32, device="cuda")   # every layer's GPU input
+    ids_a = np.zeros((STEPS, NL, K), np.uint32)
+    worst, checked = 0.0, 0
+    for s in range(STEPS):
+        st.chain_step(ctx, a, ia, wa)
+        ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
+        rec = s < E2E or s in check_steps
+        inputs = hist[s] if s < E2E else torch.zeros((NL, D), dtype=torch.float32, device="cuda")
+        st.layer_step(ctx, b, ib, wb, inputs if rec else None)
+        ctx.synchronize()
+        assert torch.equal(a, b), f"step {s}: chained step differs from the per-layer launches"
+        assert torch.equal(ia, ib) and torch.equal(wa, wb), f"step {s}: routing differs"
+        ids_a[s] = ia.cpu().numpy().view(np.uint32)
+        if s in check_steps:
+            hin = inputs.cpu().numpy()
+            gi, gw = ib.cpu().numpy().view(np.uint32), wb.cpu().numpy()
+            with O.threads(O.usable_cores()):
+                for l in range(NL):
+                    hout = hin[l + 1] if l + 1 < NL else b.cpu().numpy()
+                    worst = max(worst, check_layer(st, O, l, hin[l], hout, gi[l], gw[l]))
+                    checked += 1
+    ctx.set_decode_engine(smoe_amd.DECODE_CHAIN)
+    print(f"config 2: 256 steps bit-identical; {checked} layers teacher-forced, worst rel_err {worst:.2e}")
+    assert worst <= TOL
+
+    # end to end: the oracle on its own hidden state, step after step, until
+    # its ids first differ from the GPU's.  There the oracle applied to the
+    # GPU's own input of that layer must give the GPU's ids: the difference
+    # comes from the inputs having drifted apart (fp32 summation differences
+    # carried through the layers), not from the layer itself.
+    hist = hist.cpu().numpy()
+    h = x0.cpu().numpy().astype(np.float32)
+    first = None
+    with O.threads(O.usable_cores()):
+        for s in range(E2E):
+            for l in range(NL):
+                out, oid, _ow, logits, _n, _y = st.oracle(O, l, h)
+                if not (oid == ids_a[s, l]).all():
+                    g = hist[s, l].astype(np.float64)
+                    drift = float(np.max(np.abs(g - h)) / np.sqrt(np.mean(h.astype(np.float64) ** 2)))
+                    first = (s, l, margin_8_9(logits), drift)
+                    _o, tid, *_ = st.oracle(O, l, hist[s, l])
+                    assert (tid == ids_a[s, l]).all(), (s, l, tid, ids_a[s, l])
+                    break
+                h = out
+            if first:
+                break
+    if first is None:
+        print(f"config 2 end to end: oracle and GPU agree on every id of the first {E2E} steps")
+    else:
+        s, l, m, drift = first
+        print(f"config 2 end to end: first id difference at step {s} layer {l}: oracle rank-8/9 margin "
+              f"{m:.2e} of p8, input drift {drift:.2e} of rms; teacher-forced ids agree there")
+
+
+def test_chain_epoch_wrap_equals_layer_calls(ctx, stack30):
+    """The chain's epoch word seeded 20 below the wrap (tags of layers 19/20
+    run M, 1) and the layer kernel's 2 below it: two 48-layer chained steps in
+    a row each equal the per-layer launches bit for bit, and the epochs move
+    as the tag arithmetic says."""
+    st = stack30
+    D, K, NL = st.D, st.K, st.n
+    x0 = torch.empty(D, dtype=torch.float32, device="cuda")
+    ctx.synth_normal(x0.data_ptr(), D, SEED, smoe_amd.hidden_stream(5), 1.0)
+    ia = torch.zeros((NL, K), dtype=torch.int32, device="cuda")
+    wa = torch.zeros((NL, K), dtype=torch.float32, device="cuda")
+    ib, wb = torch.zeros_like(ia), torch.zeros_like(wa)
+    # the words exist once each kernel has run
+    tmp = x0.clone()
+    st.chain_step(ctx, tmp, ia, wa)
+    ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
+    st.layer_step(ctx, tmp, ib, wb)
+    ctx.synchronize()
+    for seed_chain, seed_layer in ((M - 20, M - 2), (M - 1, M - 30), (M, 0xFFFFFFFF)):
+        ctx.exchange_epoch(set_chain=seed_chain, set_layer=seed_layer)
+        a, b = x0.clone(), x0.clone()
+        ec, el = seed_chain, seed_layer
+        for rep in range(2):
+            st.chain_step(ctx, a, ia, wa)
+            ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
+            st.layer_step(ctx, b, ib, wb)
+            ctx.synchronize()
+            assert torch.equal(a, b), (seed_chain, rep)
+            assert torch.equal(ia, ib) and torch.equal(wa, wb), (seed_chain, rep)
+            _, _, ec = smoe_amd.exchange_tags(ec, NL)
+            _, _, el = smoe_amd.exchange_tags(el, NL)     # NL one-layer launches advance it by NL
+            got_c, got_l = ctx.exchange_epoch()
+            assert (got_c, got_l) == (ec, el), ((got_c, got_l), (ec, el))
+    ctx.set_decode_engine(smoe_amd.DECODE_CHAIN)
+
+
+def test_config3_94_layers_full_pool(ctx, oracle, stack30):
+    """Config 3: 94 235B-shaped layers resident at once (~120.6 GB of experts
+    in one pool); one chained step equals the 94 per-layer launches bit for
+    bit, and layers 0, 47 and 93 agree with the oracle on their GPU inputs."""
+    O = oracle
+    stack30.pool = None       # make room (the 30B stack is not used here)
+    torch.cuda.empty_cache()
+    st = Stack(ctx, 4096, 128, 8, 1536, 94)
+    assert st.pool.numel() >= 120_000_000_000
+    D, K, NL = st.D, st.K, st.n
+    x0 = torch.empty(D, dtype=torch.float32, device="cuda")
+    ctx.synth_normal(x0.data_ptr(), D, SEED, smoe_amd.hidden_stream(0), 1.0)
+    a, b = x0.clone(), x0.clone()
+    ia = torch.zeros((NL, K), dtype=torch.int32, device="cuda")
+    wa = torch.zeros((NL, K), dtype=torch.float32, device="cuda")
+    ib, wb = torch.zeros_like(ia), torch.zeros_like(wa)
+    inputs = torch.zeros((NL, D), dtype=torch.float32, device="cuda")
+    ctx.profile_enable(True)
+    st.chain_step(ctx, a, ia, wa)
+    ctx.synchronize()
+    n_chain, _ = ctx.profile_read(smoe_amd.KERNEL_CHAIN)
+    ctx.profile_enable(False)
+    assert n_chain == 1, "the 235B step did not run as one chained launch"
+    ctx.set_decode_engine(smoe_amd.DECODE_LAUNCHES)
+    st.layer_step(ctx, b, ib, wb, inputs)
+    ctx.synchronize()
+    ctx.set_decode_engine(smoe_amd.DECODE_CHAIN)
+    assert torch.equal(a, b) and torch.equal(ia, ib) and torch.equal(wa, wb)
+    hin = inputs.cpu().numpy()
+    gi, gw = ib.cpu().numpy().view(np.uint32), wb.cpu().numpy()
+    worst = 0.0
+    with O.threads(O.usable_cores()):
+        for l in (0, 47, 93):
+            hout = hin[l + 1] if l + 1 < NL else b.cpu().numpy()
+            worst = max(worst, check_layer(st, O, l, hin[l], hout, gi[l], gw[l]))
+    print(f"config 3: 94-layer step bit-identical to per-layer launches; layers 0/47/93 worst rel_err {worst:.2e}")
+    assert worst <= TOL
+    st.pool = None
+    torch.cuda.empty_cache()

@@ -1,7 +1,6 @@
 """The whole-stack decode step (smoe_hip_moe_decode_stack: the decode.cpp:121
 layer loop) against the CPU oracle of decode.cpp:236-509, layer by layer, for
-both engines: one persistent launch per step, and two launches per layer with
-the next layer's router read ahead.  Top-k ids must be bit-exact; the MoE
+both engines: the chained launch (one per step) and per-layer calls.  Top-k ids must be bit-exact; the MoE
 delta and the post-residual hidden state within 1e-3 per element (rel_err
 metric).  A multi-layer call must equal the same layers run one call at a time
 bit for bit (each layer's input is the previous layer's fp32 output either
@@ -15,10 +14,10 @@ from gpu_helpers import Layer, hidden_states, moe_delta_err, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
-ENGINES = [smoe_amd.DECODE_PERSISTENT, smoe_amd.DECODE_LAUNCHES, smoe_amd.DECODE_CHAIN]
+ENGINES = [smoe_amd.DECODE_LAUNCHES, smoe_amd.DECODE_CHAIN]
 
 
-@pytest.fixture(params=ENGINES, ids=["persistent", "launches", "chain"])
+@pytest.fixture(params=ENGINES, ids=["launches", "chain"])
 def engine(ctx, request):
     ctx.set_decode_engine(request.param)
     yield request.param
@@ -63,23 +62,10 @@ def test_stack_single_layer_vs_oracle(ctx, oracle, engine, D, E, K, I, norm):
         assert check_layer(oracle, layer, h0, hid.cpu().numpy(), gids[0], gw[0]) <= TOL
 
 
-@pytest.mark.skip(reason="the persistent kernel's d_model > 2048 variant is removed: it faulted once on MI355X "
-                         "(memory aperture violation) with no cause shown, and its combine stage staged only 16 "
-                         "rows per wave where d_model 4096 needs 32 (wrong values for half the rows); such shapes "
-                         "take the per-layer path (test_stack_235b_shape_per_layer_path)")
-def test_stack_235b_layer(ctx, oracle):
-    """Config 3 shape: one Qwen3-235B-A22B-shaped layer through the stack kernel."""
-    layer = Layer(ctx, 4096, 128, 8, 1536, layer_id=7)
-    hid = hidden_states(ctx, 1, 4096, 3)[0]
-    h0 = hid.cpu().numpy()
-    gids, gw = run_stack(ctx, [layer], hid)
-    assert check_layer(oracle, layer, h0, hid.cpu().numpy(), gids[0], gw[0]) <= TOL
-
-
 def test_stack_235b_shape_per_layer_path(ctx, oracle, engine):
-    """Config 3 shape through smoe_hip_moe_decode_stack: shapes outside the
-    persistent kernel run as per-layer decode calls, two layers here, each
-    checked against the oracle on the GPU's own input."""
+    """Config 3 shape through smoe_hip_moe_decode_stack, two layers, each
+    checked against the oracle on the GPU's own input of that layer, and the
+    stack call bit-identical to one-layer calls."""
     layers = [Layer(ctx, 4096, 128, 8, 1536, layer_id=7 + i) for i in range(2)]
     x0 = hidden_states(ctx, 1, 4096, 3)[0]
     full = x0.clone()
@@ -115,7 +101,7 @@ def test_stack_multi_layer_teacher_forced(ctx, oracle, engine):
 def test_stack_matches_per_layer_decode(ctx, engine):
     """The stack call and per-layer smoe_hip_moe_decode calls implement one
     MoE block: same ids, hidden states within the tolerance of each other
-    (bit-identical for the launch engine, which runs the same kernels)."""
+    (bit-identical: both engines run the one-launch layer's schedule)."""
     layers = [Layer(ctx, 2048, 128, 8, 768, layer_id=30 + i, host=False) for i in range(3)]
     x0 = hidden_states(ctx, 1, 2048, 12)[0]
     a = x0.clone()
@@ -126,8 +112,7 @@ def test_stack_matches_per_layer_decode(ctx, engine):
         ctx.moe_decode(l.shape, l.layer, b.data_ptr(), 1, ids[i].data_ptr())
     ctx.synchronize()
     assert (ids.cpu().numpy().view(np.uint32) == fids).all()
-    if engine in (smoe_amd.DECODE_LAUNCHES, smoe_amd.DECODE_CHAIN):
-        assert torch.equal(a, b)
+    assert torch.equal(a, b)
     x = x0.cpu().numpy().astype(np.float64)
     da, db = a.cpu().numpy() - x, b.cpu().numpy() - x
     slack = np.spacing(np.abs(a.cpu().numpy())) + np.spacing(np.abs(b.cpu().numpy()))

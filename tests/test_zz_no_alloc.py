@@ -61,3 +61,49 @@ def test_static_decode_rejects_large_shapes(ctx):
         assert rc == smoe_amd.SMOE_ERR_CAPACITY
     assert lib.smoe_hip_moe_decode_static(None, C.byref(lay), h.data_ptr(), None, None, None, stream) == \
         smoe_amd.SMOE_ERR_ARG
+
+
+@pytest.mark.parametrize("D,E,K,I", [
+    (2048, 128, 8, 768),     # one launch (k = 8)
+    (1024, 64, 4, 512),      # two launches (k != 8)
+])
+def test_static_decode_graph_replay(ctx, D, E, K, I):
+    """The static call captured into a graph (its scratch already set up by
+    smoe_metal_init): replays with eager static calls between them, each
+    replay bit-identical to smoe_hip_moe_decode on the same input."""
+    layer = Layer(ctx, D, E, K, I, layer_id=400 + K, host=False)
+    x0 = hidden_states(ctx, 1, D, index0=21)[0]
+    ref = x0.clone()
+    rid = torch.zeros(K, dtype=torch.int32, device="cuda")
+    rw = torch.zeros(K, dtype=torch.float32, device="cuda")
+    ctx.moe_decode(layer.shape, layer.layer, ref.data_ptr(), 1, rid.data_ptr(), rw.data_ptr())
+    ctx.synchronize()
+    buf = x0.clone()
+    ids = torch.full((K,), -1, dtype=torch.int32, device="cuda")
+    w = torch.full((K,), -1.0, dtype=torch.float32, device="cuda")
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            rc = smoe_amd.lib().smoe_hip_moe_decode_static(C.byref(layer.shape), C.byref(layer.layer),
+                                                           buf.data_ptr(), ids.data_ptr(), w.data_ptr(),
+                                                           err.data_ptr(), s.cuda_stream)
+    assert rc == smoe_amd.SMOE_OK
+    for rep in range(4):
+        buf.copy_(x0)
+        ids.fill_(-1)
+        w.fill_(-1.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        assert torch.equal(ids, rid) and torch.equal(w, rw), rep
+        assert torch.equal(buf, ref), (rep, float((buf - ref).abs().max()))
+        # eager work on the same scratch between replays
+        junk = hidden_states(ctx, 1, D, index0=40 + rep)[0]
+        ji, jw = torch.zeros_like(ids), torch.zeros_like(w)
+        assert static_decode(layer, junk, ji, jw, err) == smoe_amd.SMOE_OK
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
