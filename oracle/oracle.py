@@ -82,6 +82,8 @@ def lib():
         L.orc_silu.argtypes = [C.c_float]
         L.orc_expert_ffn.argtypes = [_u8p, _u16p, _u8p, _u16p, _u8p, _u16p, _f32p, _f32p,
                                      _f32p, C.c_uint32, C.c_uint32, C.c_uint32]
+        L.orc_expert_ffn_decode.argtypes = [_u8p, _u16p, _u8p, _u16p, _u8p, _u16p, _f32p, _f32p,
+                                     _f32p, C.c_uint32, C.c_uint32, C.c_uint32]
         L.orc_blob_layout.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32,
                                       C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
         L.orc_moe_decode_layer.argtypes = [C.POINTER(OrcShape), C.POINTER(OrcLayer), _f32p,
@@ -233,8 +235,10 @@ def top_k(scores, k, norm_topk=False):
     return ids[:cnt], w[:cnt]
 
 
-def expert_ffn(blob, off, D, I, x, group=64):
-    """Run one expert given its blob bytes and the 6 offsets."""
+def expert_ffn(blob, off, D, I, x, group=64, decode=False):
+    """Run one expert given its blob bytes and the 6 offsets: the prefill
+    token-batch arithmetic (orc_expert_ffn), or with decode=True the decode
+    path's (orc_expert_ffn_decode, kernels.metal:159-365)."""
     blob = np.ascontiguousarray(blob, np.uint8)
 
     def u8(o, n):
@@ -246,9 +250,10 @@ def expert_ffn(blob, off, D, I, x, group=64):
     n = D * I
     h = np.empty(I, np.float32)
     y = np.empty(D, np.float32)
-    lib().orc_expert_ffn(u8(off[0], n // 2), u16(off[1], n // group), u8(off[2], n // 2),
-                         u16(off[3], n // group), u8(off[4], n // 2), u16(off[5], n // group),
-                         np.ascontiguousarray(x, np.float32), h, y, I, D, group)
+    fn = lib().orc_expert_ffn_decode if decode else lib().orc_expert_ffn
+    fn(u8(off[0], n // 2), u16(off[1], n // group), u8(off[2], n // 2),
+       u16(off[3], n // group), u8(off[4], n // 2), u16(off[5], n // group),
+       np.ascontiguousarray(x, np.float32), h, y, I, D, group)
     return h, y
 
 

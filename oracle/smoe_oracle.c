@@ -355,6 +355,117 @@ void orc_expert_ffn(const uint8_t* pg, const uint16_t* sg,
     }
 }
 
+/* ------------------------------------------------------------------------ */
+/* A5-A7 on the decode path: smoe_gate_up / smoe_down (kernels.metal:308-365) */
+/* over qrow_dot2 / qrow_dot (kernels.metal:159-305), the arithmetic that     */
+/* decode.cpp:386-392's smoe_metal_fused_ffn_group dispatches.  One 32-lane    */
+/* simdgroup per row: lane L owns the 16-byte chunks c = L, L + 32, ... (32    */
+/* codes each, one scale per chunk); per chunk a float4 accumulator takes      */
+/* fma(code, x) over the chunk's 4 words (low 4 codes, then high 4, of each),  */
+/* xs += xlo + xhi, and the lane accumulator takes                              */
+/* fma(s, (a.x + a.y + a.z + a.w) * (1/7.5) - X, acc); simd_sum closes the     */
+/* row.  simd_sum's internal order is Apple's: it is restated here as an xor  */
+/* butterfly over the 32 lanes (16, 8, 4, 2, 1), and the source's operations  */
+/* are kept as written (no contraction beyond the explicit fma calls).         */
+/* ------------------------------------------------------------------------ */
+static float simd_sum32(float* v)
+{
+    for (int m = 16; m >= 1; m >>= 1) {
+        float t[32];
+        for (int l = 0; l < 32; ++l) t[l] = v[l] + v[l ^ m];
+        memcpy(v, t, sizeof t);
+    }
+    return v[0];
+}
+
+/* The row dots below come in two clones picked at load time: one for hosts
+ * with FMA instructions and a generic one, where fmaf is libm's.  Both round
+ * every fmaf once, so they give the same bits; the clone only makes the
+ * timed CPU baseline use the host's fused multiply-add. */
+#if defined(__x86_64__) && defined(__GNUC__) && !defined(__clang__)
+#define ORC_FMA_CLONES __attribute__((target_clones("fma", "default")))
+#else
+#define ORC_FMA_CLONES
+#endif
+
+/* one 32-code chunk: the float4 code.x accumulator a[4] and the x sum xs[4]
+ * (kernels.metal:183-197 / 266-287) */
+static inline __attribute__((always_inline)) void q4_chunk(const uint8_t* chunk, const float* xv, float a[4], float xs[4])
+{
+    for (int k = 0; k < 4; ++k) {
+        uint32_t u = (uint32_t)chunk[4 * k] | ((uint32_t)chunk[4 * k + 1] << 8) |
+                     ((uint32_t)chunk[4 * k + 2] << 16) | ((uint32_t)chunk[4 * k + 3] << 24);
+        const float* xlo = xv + 8 * k;
+        const float* xhi = xv + 8 * k + 4;
+        for (int j = 0; j < 4; ++j) a[j] = fmaf((float)((u >> (4 * j)) & 0xFu), xlo[j], a[j]);
+        for (int j = 0; j < 4; ++j) a[j] = fmaf((float)((u >> (16 + 4 * j)) & 0xFu), xhi[j], a[j]);
+        for (int j = 0; j < 4; ++j) xs[j] = xs[j] + (xlo[j] + xhi[j]);
+    }
+}
+
+ORC_FMA_CLONES static float q4_qrow_dot(const uint8_t* packed, const uint16_t* scales, size_t row, uint32_t cols,
+                         uint32_t group, const float* x)
+{
+    const uint8_t* rp = packed + row * (size_t)(cols >> 1);
+    const uint16_t* srow = scales + row * (size_t)(cols / group);
+    const uint32_t nchunks = cols >> 5;
+    float acc[32] = {0};
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        float a[4] = {0, 0, 0, 0}, xs[4] = {0, 0, 0, 0};
+        q4_chunk(rp + 16 * (size_t)c, x + 32 * (size_t)c, a, xs);
+        const float s = orc_f16_to_f32(srow[(c << 5) / group]);
+        const float A = ((a[0] + a[1]) + a[2]) + a[3];
+        const float X = ((xs[0] + xs[1]) + xs[2]) + xs[3];
+        acc[c & 31u] = fmaf(s, A * (1.0f / 7.5f) - X, acc[c & 31u]);
+    }
+    return simd_sum32(acc);
+}
+
+ORC_FMA_CLONES static void q4_qrow_dot2(const uint8_t* gp, const uint16_t* gs, const uint8_t* up, const uint16_t* us,
+                         size_t row, uint32_t cols, uint32_t group, const float* x, float* g_out, float* u_out)
+{
+    const size_t rb = row * (size_t)(cols >> 1), sbase = row * (size_t)(cols / group);
+    const uint32_t nchunks = cols >> 5;
+    float ga[32] = {0}, ua[32] = {0};
+    for (uint32_t c = 0; c < nchunks; ++c) {
+        float ag[4] = {0, 0, 0, 0}, au[4] = {0, 0, 0, 0}, xs[4] = {0, 0, 0, 0}, xs2[4] = {0, 0, 0, 0};
+        q4_chunk(gp + rb + 16 * (size_t)c, x + 32 * (size_t)c, ag, xs);
+        q4_chunk(up + rb + 16 * (size_t)c, x + 32 * (size_t)c, au, xs2);   /* (xs2 == xs) */
+        const float sg = orc_f16_to_f32(gs[sbase + (c << 5) / group]);
+        const float su = orc_f16_to_f32(us[sbase + (c << 5) / group]);
+        const float X = ((xs[0] + xs[1]) + xs[2]) + xs[3];
+        ga[c & 31u] = fmaf(sg, (((ag[0] + ag[1]) + ag[2]) + ag[3]) * (1.0f / 7.5f) - X, ga[c & 31u]);
+        ua[c & 31u] = fmaf(su, (((au[0] + au[1]) + au[2]) + au[3]) * (1.0f / 7.5f) - X, ua[c & 31u]);
+    }
+    *g_out = simd_sum32(ga);
+    *u_out = simd_sum32(ua);
+}
+
+static void expert_ffn_decode_rows(const uint8_t* pg, const uint16_t* sg, const uint8_t* pu, const uint16_t* su,
+                                   const uint8_t* pd, const uint16_t* sd, const float* x, float* hidden,
+                                   float* out, uint32_t d_ff, uint32_t d_model, uint32_t group, int parallel)
+{
+#pragma omp parallel num_threads(g_threads) if (parallel && g_threads > 1)
+    {
+#pragma omp for schedule(static)
+        for (uint32_t r = 0; r < d_ff; ++r) {
+            float g, u;
+            q4_qrow_dot2(pg, sg, pu, su, r, d_model, group, x, &g, &u);
+            hidden[r] = orc_silu(g) * u;                   /* kernels.metal:333-335 */
+        }
+#pragma omp for schedule(static)
+        for (uint32_t d = 0; d < d_model; ++d)
+            out[d] = q4_qrow_dot(pd, sd, d, d_ff, group, hidden);   /* kernels.metal:360-364 */
+    }
+}
+
+void orc_expert_ffn_decode(const uint8_t* pg, const uint16_t* sg, const uint8_t* pu, const uint16_t* su,
+                           const uint8_t* pd, const uint16_t* sd, const float* x, float* hidden, float* out,
+                           uint32_t d_ff, uint32_t d_model, uint32_t group)
+{
+    expert_ffn_decode_rows(pg, sg, pu, su, pd, sd, x, hidden, out, d_ff, d_model, group, 1);
+}
+
 /* The same FFN with one thread, for callers that already run in parallel. */
 static void expert_ffn_serial(const uint8_t* pg, const uint16_t* sg, const uint8_t* pu, const uint16_t* su,
                               const uint8_t* pd, const uint16_t* sd, const float* x, float* hidden, float* out,
@@ -422,7 +533,7 @@ void orc_moe_decode_layer(const OrcShape* s, const OrcLayer* L, float* hidden,
     for (uint32_t e = 0; e < nk; ++e) {                        /* :482-498 */
         const uint8_t *pg, *pu, *pd; const uint16_t *sg, *su, *sd;
         expert_ptrs(L, rid[e], &pg, &sg, &pu, &su, &pd, &sd);
-        orc_expert_ffn(pg, sg, pu, su, pd, sd, normed, h, y, I, D, s->group_size);
+        orc_expert_ffn_decode(pg, sg, pu, su, pd, sd, normed, h, y, I, D, s->group_size);
         if (expert_out) memcpy(expert_out + (size_t)e * D, y, D * sizeof(float));
         orc_axpy_f32(routed, w[e], y, D);
     }

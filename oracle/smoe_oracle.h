@@ -18,11 +18,19 @@
  *       src/compute/kernels.metal:90-105
  *       pinned: known-answer tests (+-absmax -> 15/0, half-even ties, zero
  *       group, nibble order, reconstruction bound), numpy float16 cast.
- *   orc_expert_ffn   kernels.metal:61-63, 308-365, 672-769
- *       pinned: fp64 brute force on tiny shapes, dequant identity, zero
- *       input, scale linearity.  (The reference's FFN exists only as Metal
- *       shaders; no reference-held vectors exist.)
- *   orc_moe_decode_layer   src/decode.cpp:236-238, 280-302, 338-509
+ *   orc_expert_ffn   kernels.metal:61-63, 90-105, 672-769 (prefill's
+ *       token-batch kernels: per-weight dequant, sequential fp32 sums)
+ *   orc_expert_ffn_decode   kernels.metal:61-63, 159-365 (the decode path's
+ *       qrow_dot2 / qrow_dot: lane-strided chunks, affine chunk epilogue,
+ *       simd_sum)
+ *       both pinned: fp64 brute force on tiny and Qwen3-sized shapes (the
+ *       decode form within a bound that a dropped chunk, a wrong lane
+ *       stride, scale or nibble order exceeds), dequant identity, zero input,
+ *       scale linearity.  (The reference's FFN exists only as Metal shaders;
+ *       no reference-held vectors exist, and the order inside Metal's
+ *       simd_sum and any fast-math contraction are parity unpinned.)
+ *   orc_moe_decode_layer   src/decode.cpp:236-238, 280-302, 338-509 (its
+ *       expert FFN is orc_expert_ffn_decode)
  *   orc_permute / orc_union_*   src/prefill.cpp:38-68, 315-332
  *       pinned: compiled reference union_add vectors; brute-force stable sort.
  *   orc_moe_prefill_layer  src/prefill.cpp:308-453
@@ -86,13 +94,23 @@ void orc_axpy_f32(float* y, float a, const float* x, uint32_t n);
 uint32_t orc_top_k(const float* scores, uint32_t n, uint32_t k,
                    uint32_t* out_indices, float* out_weights, int norm_topk);
 
-/* ---- A5/A6: one expert, per-weight dequant, sequential fp32 sums ---------- */
+/* ---- A5/A6: one expert, per-weight dequant, sequential fp32 sums (the
+ *      token-batch kernels of prefill, kernels.metal:672-769) ------------- */
 float orc_silu(float x);
 void orc_expert_ffn(const uint8_t* pg, const uint16_t* sg,
                     const uint8_t* pu, const uint16_t* su,
                     const uint8_t* pd, const uint16_t* sd,
                     const float* x, float* hidden, float* out,
                     uint32_t d_ff, uint32_t d_model, uint32_t group);
+/* ---- A5-A7: one expert as the decode path computes it: smoe_gate_up and
+ *      smoe_down over qrow_dot2 / qrow_dot (kernels.metal:159-365): lane-
+ *      strided 32-code chunks with the affine chunk epilogue, simd_sum per
+ *      row.  cols % 32 == 0, group % 32 == 0. -------------------------------- */
+void orc_expert_ffn_decode(const uint8_t* pg, const uint16_t* sg,
+                           const uint8_t* pu, const uint16_t* su,
+                           const uint8_t* pd, const uint16_t* sd,
+                           const float* x, float* hidden, float* out,
+                           uint32_t d_ff, uint32_t d_model, uint32_t group);
 
 /* ---- A11: resident expert pool addressing -------------------------------- */
 typedef struct {

@@ -88,20 +88,20 @@ def run_prefill(ctx, layer, T, index0=0, perm=False, h=None):
 F64_TOL = 5e-4
 
 
-def check_against_oracle(oracle, layer, h0, got, gids, gw, rows=None, exact=False):
+def check_against_oracle(oracle, layer, h0, got, gids, gw, rows=None, exact=False, credit=False):
     """Worst relative error of the GPU's MoE delta against the oracle's over
     `rows`, after asserting their ids / weights.
 
     With exact=True every checked token is also evaluated in fp64 (same ids
-    and weights) and two things are asserted or returned:
-      * the GPU delta within F64_TOL of the fp64 delta (asserted);
-      * against the oracle, the excess of |gpu - oracle| over the oracle's
-        own distance from fp64 at that element (returned): at d_model 4096
-        the oracle's sequential fp32 sums over 4096 and 1536 terms -- the
-        reference's batch-kernel arithmetic, kernels.metal:672-769 -- round
-        to up to ~1e-3 of an element near the 1 % floor, more than the
-        kernels do, so the plain distance can exceed 1e-3 while the GPU is the
-        closer of the two to the exact value."""
+    and weights), and the GPU delta must lie within F64_TOL of the fp64 delta
+    (asserted).  The plain distance to the oracle is returned, unless
+    credit=True: then the excess of |gpu - oracle| over the oracle's own
+    distance from fp64 at that element is returned instead.  That is for
+    shapes where the oracle's sequential fp32 sums over 4096 and 1536 terms --
+    the reference's batch-kernel arithmetic, kernels.metal:672-769 -- round to
+    ~1e-3 of an element near the 1 % floor, more than the kernels do, so the
+    plain distance can exceed 1e-3 while the GPU is the closer of the two to
+    the exact value."""
     rows = np.arange(h0.shape[0]) if rows is None else rows
     # (threaded oracle: bit-identical to its single-threaded loops)
     with oracle.threads(oracle.usable_cores()):
@@ -127,10 +127,10 @@ def check_against_oracle(oracle, layer, h0, got, gids, gw, rows=None, exact=Fals
         w64 = max(w64, rel_err(d_got[i], x64[i], slack=sl)[0])
         w_orc = max(w_orc, rel_err(d_ref[i], x64[i], slack=np.spacing(np.abs(ref[i])).astype(np.float64))[0])
         w_cred = max(w_cred, rel_err(d_got[i], d_ref[i], slack=slack[i] + np.abs(d_ref[i] - x64[i]))[0])
-    print(f"prefill vs fp64: gpu {w64:.2e}, oracle {w_orc:.2e}; gpu vs oracle beyond the oracle's own "
-          f"rounding {w_cred:.2e}")
+    print(f"prefill vs fp64: gpu {w64:.2e}, oracle {w_orc:.2e}; gpu vs oracle {worst:.2e} plain, "
+          f"{w_cred:.2e} beyond the oracle's own rounding")
     assert w64 <= F64_TOL
-    return w_cred
+    return w_cred if credit else worst
 
 
 def test_prefill_tiny_shapes(ctx, oracle):
@@ -182,8 +182,13 @@ def test_prefill_235b_512_tokens(ctx, oracle):
     """512 tokens through one 235B-shaped layer (D=4096, I=1536): about 32
     pairs per expert, so the grouped GEMM runs its 32- and 48-pair pass widths
     over 64 groups.  Every token's ids exact; the hidden update on 64 tokens
-    spread over the batch (tokens are independent inside the block) against
-    the oracle and an fp64 evaluation (check_against_oracle, exact=True)."""
+    spread over the batch (tokens are independent inside the block) within
+    5e-4 of an fp64 evaluation and within 1e-3 of the oracle beyond the
+    oracle's own rounding (check_against_oracle, exact=True, credit=True: the
+    oracle, which restates the reference's token-batch kernels with one
+    sequential fp32 sum per row, is itself up to 1.7e-3 from fp64 on these 64
+    tokens, and the plain GPU-oracle distance follows it to 1.6e-3, while the
+    GPU stays within 1.5e-4 of fp64)."""
     layer = Layer(ctx, 4096, 128, 8, 1536, layer_id=13)
     T = 512
     h0, got, gids, gw, _ = run_prefill(ctx, layer, T, index0=2000)
@@ -194,7 +199,7 @@ def test_prefill_235b_512_tokens(ctx, oracle):
         assert (gids[t] == rid).all(), t
         assert np.allclose(gw[t], rw, rtol=1e-5, atol=1e-7)
     rows = np.linspace(0, T - 1, 64).astype(int)
-    assert check_against_oracle(oracle, layer, h0, got, gids, gw, rows=rows, exact=True) <= TOL
+    assert check_against_oracle(oracle, layer, h0, got, gids, gw, rows=rows, exact=True, credit=True) <= TOL
 
 
 def test_batched_235b_zipf_64_tokens(ctx, oracle):
@@ -206,7 +211,7 @@ def test_batched_235b_zipf_64_tokens(ctx, oracle):
     reference's token-batch FFN plus its per-token fallback,
     prefill.cpp:339-417, metal_bridge.mm:544-634).  All 64 tokens: ids
     bit-exact, hidden update within 5e-4 of an fp64 evaluation and within
-    1e-3 of the oracle beyond the oracle's own rounding (check_against_oracle)."""
+    1e-3 of the oracle (check_against_oracle, exact=True)."""
     from smoe_amd import synthetic
     D, E, K, I, T = 4096, 128, 8, 1536, 64
     layer = Layer(ctx, D, E, K, I, layer_id=0, host=False)
@@ -306,8 +311,10 @@ def test_route_block_shapes(ctx, oracle, D, E, K, I, T):
     normalised by one wave each and handed to the others through LDS.  Every
     token's ids and weights against the oracle's router + top-k; the hidden
     update of 32 tokens spread over the batch against an fp64 evaluation and
-    the oracle (check_against_oracle, exact=True: at d_model 4096 the oracle's
-    own fp32 rounding exceeds the plain 1e-3 bound, as in the 235B tests)."""
+    the oracle (check_against_oracle, exact=True, credit=True: with 32 of the
+    tokens at d_model 4096 the oracle's own fp32 rounding reaches 1.3e-3 of an
+    element near the floor, above the plain 1e-3 bound, while the kernels stay
+    within 1.1e-4 of fp64)."""
     layer = Layer(ctx, D, E, K, I, layer_id=300 + D // 64 + T)
     h0, got, gids, gw, _ = run_prefill(ctx, layer, T, index0=3000)
     for t in range(T):
@@ -317,4 +324,4 @@ def test_route_block_shapes(ctx, oracle, D, E, K, I, T):
         assert (gids[t] == rid).all(), t
         assert np.allclose(gw[t], rw, rtol=1e-5, atol=1e-7), t
     rows = np.linspace(0, T - 1, 32).astype(int)
-    assert check_against_oracle(oracle, layer, h0, got, gids, gw, rows=rows, exact=True) <= TOL
+    assert check_against_oracle(oracle, layer, h0, got, gids, gw, rows=rows, exact=True, credit=True) <= TOL
