@@ -57,7 +57,8 @@ def kernel_bytes(c):
     whole-step kernels (per layer the same bytes as one k_moe_layer launch:
     k * B_expert + 2 E D router + 2 D norm weights + 4 D hidden in + 4 D out)."""
     D, E, K, I = c["D"], c["E"], c["K"], c["I"]
-    mat = D * I // 2 + D * I // 64 * 2            # packed nibbles + fp16 scales of one matrix
+    # packed nibbles + fp16 scales of one matrix (scale+min format: + bf16 mins)
+    mat = D * I // 2 + D * I // 64 * 2 * (2 if c.get("quant") else 1)
     # the whole block: router bf16 + norm weights + 8 experts' gate/up/down + hidden in and out
     layer = K * 3 * mat + 2 * E * D + 2 * D + 8 * D
     return {
@@ -123,6 +124,9 @@ def main():
                          "smoe_hip_moe_decode call per layer")
     ap.add_argument("--no-configs", action="store_true",
                     help="decode: skip the configs block (configs 3, 4 and 5 after the headline)")
+    ap.add_argument("--quant", default="smoeq4", choices=("smoeq4", "scale_min"),
+                    help="decode: the 4-bit group format of the experts (smoeq4: the reference's fp16 absmax; "
+                         "scale_min: a bf16 scale and min per group, the configs' wording)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU work the baseline sample aims at")
     ap.add_argument("--profile-steps", type=int, default=8, help="replays of the event-timed step (0: skip)")
@@ -185,6 +189,14 @@ def configs_block(args):
     out["3"]["us_per_layer"] = round(d["ms_per_step"] * 1e3 / d["config"]["layers"], 2)
     out["3"]["parity"] = d.get("parity")
     torch.cuda.empty_cache()
+    # config 2 again in the configs' literal format (bf16 scale and min per group)
+    sub.quant = "scale_min"
+    d = decode_line(sub, "30b", 64, 8, cpu=False)
+    sub.quant = "smoeq4"
+    out["2_scale_min"] = {k: d[k] for k in ("value", "unit", "ms_per_step", "steps", "warmup", "config", "roofline",
+                                             "parity")}
+    out["2_scale_min"]["us_per_layer"] = round(d["ms_per_step"] * 1e3 / d["config"]["layers"], 2)
+    torch.cuda.empty_cache()
     for cid, wl in (("4", "prefill"), ("5", "batched")):
         g = grouped_line(wl, 4, 16, 2, 0)
         out[cid] = {k: g[k] for k in ("value", "unit", "us_per_layer_call", "layer_bytes", "layer_gbs",
@@ -205,6 +217,9 @@ def decode_line(args, cname, steps, warmup, cpu=True):
     c = dict(CONFIGS[cname])
     if args.layers:
         c["layers"] = args.layers
+    c["quant"] = smoe_amd.QUANT_Q4_SCALE_MIN if getattr(args, "quant", "smoeq4") == "scale_min" else 0
+    if c["quant"]:
+        c["workload"] += "-scale-min"
     D, E, K, I, NL = c["D"], c["E"], c["K"], c["I"], c["layers"]
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
@@ -215,8 +230,8 @@ def decode_line(args, cname, steps, warmup, cpu=True):
 
     calibrate_copy(args, dev)
 
-    shape = smoe_amd.make_shape(D, E, K, I)
-    off, raw, stride = smoe_amd.blob_layout(D, I)
+    shape = smoe_amd.make_shape(D, E, K, I, quant=c["quant"])
+    off, raw, stride = smoe_amd.blob_layout(D, I, quant=c["quant"])
     log(f"generating {NL} layers x {E} experts ({NL * E * stride / 1e9:.1f} GB) on the GPU")
     pool = torch.empty(NL * E * stride, dtype=torch.uint8, device=dev)
     t_gen = time.perf_counter()
@@ -293,7 +308,8 @@ def decode_line(args, cname, steps, warmup, cpu=True):
         "data": "synthetic (counter-based N(0,0.02) weights quantized to SMOE-Q4; N(0,1) hidden)",
         "config": {"workload": c["workload"], "d_model": D, "n_experts": E, "top_k": K, "d_ff": I,
                    "layers": NL, "batch": 1, "decode_steps": steps,
-                   "quant": "SMOE-Q4 g64 fp16 absmax", "launch": "hip-graph" if graph else "eager",
+                   "quant": "Q4 g64 bf16 scale + bf16 min" if c["quant"] else "SMOE-Q4 g64 fp16 absmax",
+                   "launch": "hip-graph" if graph else "eager",
                    "engine": {"stack": "stack API, per-layer launches",
                               "split": "stack API, two launches per layer",
                               "chain": "stack API, one launch per step running the one-launch layer schedule "
@@ -425,7 +441,7 @@ def parity_leg(ctx, c, shape, pool, router, norm_w, hidden0, stride, off, engine
 
     O = _oracle()
     D, E, K, I, NL = c["D"], c["E"], c["K"], c["I"], c["layers"]
-    oshape = dict(d_model=D, n_experts=E, top_k=K, d_ff=I, group_size=64, norm_topk=1)
+    oshape = dict(d_model=D, n_experts=E, top_k=K, d_ff=I, group_size=64, norm_topk=1, quant=c.get("quant", 0))
     h_norm = norm_w.cpu().numpy().view(np.uint16)
     lb = E * stride
     cores = O.usable_cores()
@@ -498,7 +514,7 @@ def cpu_baseline(c, pool, router, norm_w, hidden0, stride, off, target_s):
 
     O = _oracle()
     D, E, K, I, NL = c["D"], c["E"], c["K"], c["I"], c["layers"]
-    oshape = dict(d_model=D, n_experts=E, top_k=K, d_ff=I, group_size=64, norm_topk=1)
+    oshape = dict(d_model=D, n_experts=E, top_k=K, d_ff=I, group_size=64, norm_topk=1, quant=c.get("quant", 0))
     h_norm = norm_w.cpu().numpy().view(np.uint16)
     layer_bytes = E * stride
     n_cpu = NL if NL * layer_bytes <= 20e9 else 8          # layers copied to the host

@@ -192,7 +192,28 @@ typedef struct {
     uint32_t group_size;  /* SMOE quant group: must be 64 (vault format) */
     uint32_t bits;        /* must be 4                              */
     uint32_t norm_topk;   /* renormalise the k weights (Qwen3: 1)   */
+    uint32_t quant;       /* SMOE_QUANT_*: the 4-bit group format   */
 } SmoeMoeShape;
+
+/* 4-bit group formats of the expert matrices (groups of group_size
+ * consecutive weights of a row-major matrix, two codes a byte, low nibble =
+ * even index).
+ *   SMOE_QUANT_SMOEQ4: the vault's format (quantize_smoeq4, shatter_moe.py:
+ *     331-387; kernels.metal:90-105): one fp16 absmax scale s per group,
+ *     w = (code - 7.5) / 7.5 * s.  Each matrix is [packed][scales].
+ *   SMOE_QUANT_Q4_SCALE_MIN: one bf16 scale s and one bf16 min m per group,
+ *     w = code * s + m (no counterpart in the reference: the format the
+ *     benchmark configurations name).  Each matrix is [packed][scales][mins]:
+ *     the mins follow the scales of the same matrix, so the layer's six
+ *     offsets (SmoeMoeLayer) still describe a blob.  Quantizer
+ *     (smoe_hip_quantize_q4_scale_min): m = bf16(min w), s = bf16((max w -
+ *     min w) / 15) (1 when that is 0), code = clamp(rint((w - m) / s), 0, 15)
+ *     with the rounded s and m, ties to even.  Runs on the one-launch decode
+ *     kernels (top_k 8, up to 128 experts, d_model <= 2048: Qwen3-30B-A3B);
+ *     other decode shapes, SMOE_DECODE_SPLIT and prefill return
+ *     SMOE_ERR_BITS for it. */
+#define SMOE_QUANT_SMOEQ4        0
+#define SMOE_QUANT_Q4_SCALE_MIN  1
 
 /* Weights of one MoE layer, all device pointers.  Expert e's blob starts at
  * experts + e * expert_stride and holds the six tensors at the offsets of the
@@ -352,6 +373,12 @@ int smoe_hip_permute(SmoeMetalCtx* ctx, const uint32_t* ids, const float* weight
 int smoe_hip_quantize_q4(SmoeMetalCtx* ctx, const float* w, uint64_t n,
                          uint32_t group_size, uint8_t* packed, uint16_t* scales);
 
+/* The SMOE_QUANT_Q4_SCALE_MIN quantizer (above) on device: w [n] fp32 ->
+ * packed [n/2], scales [n/group_size] and mins [n/group_size] bf16 bits.  No
+ * counterpart in the reference. */
+int smoe_hip_quantize_q4_scale_min(SmoeMetalCtx* ctx, const float* w, uint64_t n, uint32_t group_size,
+                                   uint8_t* packed, uint16_t* scales, uint16_t* mins);
+
 /* ---- synthetic inputs (counter-based RNG, reproducible on the host) ----- */
 /* out[i] = stddev * N(0,1)(key(seed, stream), i) */
 int smoe_hip_synth_normal(SmoeMetalCtx* ctx, float* out, uint64_t n, uint64_t seed,
@@ -362,7 +389,9 @@ int smoe_hip_synth_bf16(SmoeMetalCtx* ctx, uint16_t* out, uint64_t n, uint64_t s
 /* n_layers x n_experts expert blobs at base + (l*n_experts + e)*expert_stride:
  * each of gate [d_ff x d_model], up, down [d_model x d_ff] drawn
  * N(0, stddev) from stream (first_layer+l)<<32 | e<<4 | m (m = 0 gate, 1 up,
- * 2 down) and quantized to SMOE-Q4 in the build_expert_blob layout. */
+ * 2 down) and quantized to the shape's format (SMOE-Q4 in the
+ * build_expert_blob layout, or scale+min with each matrix's mins after its
+ * scales). */
 int smoe_hip_synth_expert_pool(SmoeMetalCtx* ctx, uint8_t* base, uint32_t first_layer,
                                uint32_t n_layers, uint32_t n_experts,
                                uint64_t expert_stride, const SmoeMoeShape* shape,

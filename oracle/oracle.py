@@ -34,7 +34,7 @@ def build(reference_root: str | None = None) -> None:
 
 class OrcShape(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in
-                ("d_model", "n_experts", "top_k", "d_ff", "group_size", "norm_topk")]
+                ("d_model", "n_experts", "top_k", "d_ff", "group_size", "norm_topk", "quant")]
 
 
 class OrcLayer(C.Structure):
@@ -83,7 +83,12 @@ def lib():
         L.orc_expert_ffn.argtypes = [_u8p, _u16p, _u8p, _u16p, _u8p, _u16p, _f32p, _f32p,
                                      _f32p, C.c_uint32, C.c_uint32, C.c_uint32]
         L.orc_expert_ffn_decode.argtypes = [_u8p, _u16p, _u8p, _u16p, _u8p, _u16p, _f32p, _f32p,
-                                     _f32p, C.c_uint32, C.c_uint32, C.c_uint32]
+                                            _f32p, C.c_uint32, C.c_uint32, C.c_uint32]
+        L.orc_expert_ffn_decode_min.argtypes = [_u8p, _u16p, _u16p, _u8p, _u16p, _u16p, _u8p, _u16p, _u16p,
+                                                _f32p, _f32p, _f32p, C.c_uint32, C.c_uint32, C.c_uint32]
+        L.orc_quantize_q4_min.argtypes = [_f32p, C.c_size_t, C.c_uint32, _u8p, _u16p, _u16p]
+        L.orc_dequant_q4_min.restype = C.c_float
+        L.orc_dequant_q4_min.argtypes = [_u8p, _u16p, _u16p, C.c_size_t, C.c_uint32]
         L.orc_blob_layout.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32,
                                       C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
         L.orc_moe_decode_layer.argtypes = [C.POINTER(OrcShape), C.POINTER(OrcLayer), _f32p,
@@ -235,10 +240,11 @@ def top_k(scores, k, norm_topk=False):
     return ids[:cnt], w[:cnt]
 
 
-def expert_ffn(blob, off, D, I, x, group=64, decode=False):
+def expert_ffn(blob, off, D, I, x, group=64, decode=False, quant=0):
     """Run one expert given its blob bytes and the 6 offsets: the prefill
     token-batch arithmetic (orc_expert_ffn), or with decode=True the decode
-    path's (orc_expert_ffn_decode, kernels.metal:159-365)."""
+    path's (orc_expert_ffn_decode, kernels.metal:159-365); quant=1: the
+    scale+min format on the decode path's lanes and chunks."""
     blob = np.ascontiguousarray(blob, np.uint8)
 
     def u8(o, n):
@@ -250,6 +256,13 @@ def expert_ffn(blob, off, D, I, x, group=64, decode=False):
     n = D * I
     h = np.empty(I, np.float32)
     y = np.empty(D, np.float32)
+    if quant:
+        ng = n // group
+        lib().orc_expert_ffn_decode_min(u8(off[0], n // 2), u16(off[1], ng), u16(off[1] + 2 * ng, ng),
+                                        u8(off[2], n // 2), u16(off[3], ng), u16(off[3] + 2 * ng, ng),
+                                        u8(off[4], n // 2), u16(off[5], ng), u16(off[5] + 2 * ng, ng),
+                                        np.ascontiguousarray(x, np.float32), h, y, I, D, group)
+        return h, y
     fn = lib().orc_expert_ffn_decode if decode else lib().orc_expert_ffn
     fn(u8(off[0], n // 2), u16(off[1], n // group), u8(off[2], n // 2),
        u16(off[3], n // group), u8(off[4], n // 2), u16(off[5], n // group),
@@ -257,11 +270,34 @@ def expert_ffn(blob, off, D, I, x, group=64, decode=False):
     return h, y
 
 
-def blob_layout(D, I, group=64):
+def blob_layout(D, I, group=64, quant=0):
+    """Offsets of the six tensors of one expert blob and its size; quant=1
+    (the scale+min format): each matrix's mins follow its scales, inside the
+    scales' region, which doubles."""
+    if quant:
+        n = D * I
+        pb, sb = n // 2, 2 * (n // group * 2)
+        return [0, pb, pb + sb, 2 * pb + sb, 2 * (pb + sb), 3 * pb + 2 * sb], 3 * (pb + sb)
     off = (C.c_uint64 * 6)()
     nb = C.c_uint64()
     lib().orc_blob_layout(D, I, group, off, C.byref(nb))
     return [int(v) for v in off], int(nb.value)
+
+
+def quantize_q4_min(w, group=64):
+    """The scale+min format: (packed, scales, mins) of w, bf16 bits."""
+    w = np.ascontiguousarray(w, np.float32).ravel()
+    n = w.size
+    packed = np.zeros(n // 2, np.uint8)
+    scales = np.zeros(n // group, np.uint16)
+    mins = np.zeros(n // group, np.uint16)
+    lib().orc_quantize_q4_min(w, n, group, packed, scales, mins)
+    return packed, scales, mins
+
+
+def dequant_q4_min(packed, scales, mins, n, group=64):
+    p, s, m = (np.ascontiguousarray(a) for a in (packed, scales, mins))
+    return np.array([lib().orc_dequant_q4_min(p, s, m, i, group) for i in range(n)], np.float32)
 
 
 def _layer_struct(norm_w, router_w, experts, stride, off):

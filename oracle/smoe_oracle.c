@@ -219,6 +219,50 @@ void orc_dequant_q4_all(const uint8_t* packed, const uint16_t* scales, size_t n,
     for (size_t i = 0; i < n; ++i) out[i] = orc_dequant_q4(packed, scales, i, group);
 }
 
+/* The scale+min format of the benchmark configurations (no counterpart in
+ * the reference; this build's definition, the one the GPU quantizer uses):
+ * per group m = bf16(min w), s = bf16((max w - min w) / 15) (bf16 1.0 when
+ * that rounds to 0), code = clamp(rint((w - m) / s), 0, 15) from the rounded
+ * s and m (two roundings: the difference, then the quotient), low nibble =
+ * even index.  Dequant: w = code * s + m. */
+void orc_quantize_q4_min(const float* w, size_t n, uint32_t group, uint8_t* packed, uint16_t* scales,
+                         uint16_t* mins)
+{
+    size_t n_groups = n / group;
+    memset(packed, 0, n / 2);
+    for (size_t g = 0; g < n_groups; ++g) {
+        const float* v = w + g * (size_t)group;
+        float lo = v[0], hi = v[0];
+        for (uint32_t j = 1; j < group; ++j) {
+            if (v[j] < lo) lo = v[j];
+            if (v[j] > hi) hi = v[j];
+        }
+        float span = (hi - lo) / 15.0f;
+        uint16_t sb = orc_f32_to_bf16(span);
+        if ((sb & 0x7FFFu) == 0) sb = 0x3F80u;
+        uint16_t mb = orc_f32_to_bf16(lo);
+        scales[g] = sb;
+        mins[g] = mb;
+        float s = orc_bf16_to_f32(sb), m = orc_bf16_to_f32(mb);
+        for (uint32_t j = 0; j < group; ++j) {
+            float q = v[j] - m;
+            q = q / s;
+            int c = (int)rintf(q);
+            if (c < 0) c = 0;
+            if (c > 15) c = 15;
+            size_t i = g * (size_t)group + j;
+            packed[i >> 1] |= (uint8_t)((uint32_t)c << ((i & 1u) * 4u));
+        }
+    }
+}
+
+float orc_dequant_q4_min(const uint8_t* packed, const uint16_t* scales, const uint16_t* mins, size_t wi,
+                         uint32_t group)
+{
+    uint32_t code = ((uint32_t)packed[wi >> 1] >> ((wi & 1u) * 4u)) & 0xFu;
+    return (float)code * orc_bf16_to_f32(scales[wi / group]) + orc_bf16_to_f32(mins[wi / group]);
+}
+
 void orc_synth_q4(uint8_t* packed, uint16_t* scales, uint32_t rows, uint32_t cols,
                   uint32_t group, uint64_t seed, uint64_t stream, float stddev)
 {
@@ -403,26 +447,35 @@ static inline __attribute__((always_inline)) void q4_chunk(const uint8_t* chunk,
     }
 }
 
-ORC_FMA_CLONES static float q4_qrow_dot(const uint8_t* packed, const uint16_t* scales, size_t row, uint32_t cols,
-                         uint32_t group, const float* x)
+/* mins: NULL for SMOE-Q4; else the scale+min format, whose chunk value is
+ * s * A + m * X (the same lanes, chunks and sums; the epilogue of w = c s + m) */
+ORC_FMA_CLONES static float q4_qrow_dot(const uint8_t* packed, const uint16_t* scales, const uint16_t* mins,
+                                        size_t row, uint32_t cols, uint32_t group, const float* x)
 {
     const uint8_t* rp = packed + row * (size_t)(cols >> 1);
     const uint16_t* srow = scales + row * (size_t)(cols / group);
+    const uint16_t* mrow = mins ? mins + row * (size_t)(cols / group) : NULL;
     const uint32_t nchunks = cols >> 5;
     float acc[32] = {0};
     for (uint32_t c = 0; c < nchunks; ++c) {
         float a[4] = {0, 0, 0, 0}, xs[4] = {0, 0, 0, 0};
         q4_chunk(rp + 16 * (size_t)c, x + 32 * (size_t)c, a, xs);
-        const float s = orc_f16_to_f32(srow[(c << 5) / group]);
         const float A = ((a[0] + a[1]) + a[2]) + a[3];
         const float X = ((xs[0] + xs[1]) + xs[2]) + xs[3];
-        acc[c & 31u] = fmaf(s, A * (1.0f / 7.5f) - X, acc[c & 31u]);
+        if (mrow) {
+            const float s = orc_bf16_to_f32(srow[(c << 5) / group]), m = orc_bf16_to_f32(mrow[(c << 5) / group]);
+            acc[c & 31u] = fmaf(s, A, fmaf(m, X, acc[c & 31u]));
+        } else {
+            const float s = orc_f16_to_f32(srow[(c << 5) / group]);
+            acc[c & 31u] = fmaf(s, A * (1.0f / 7.5f) - X, acc[c & 31u]);
+        }
     }
     return simd_sum32(acc);
 }
 
-ORC_FMA_CLONES static void q4_qrow_dot2(const uint8_t* gp, const uint16_t* gs, const uint8_t* up, const uint16_t* us,
-                         size_t row, uint32_t cols, uint32_t group, const float* x, float* g_out, float* u_out)
+ORC_FMA_CLONES static void q4_qrow_dot2(const uint8_t* gp, const uint16_t* gs, const uint16_t* gm, const uint8_t* up,
+                                        const uint16_t* us, const uint16_t* um, size_t row, uint32_t cols,
+                                        uint32_t group, const float* x, float* g_out, float* u_out)
 {
     const size_t rb = row * (size_t)(cols >> 1), sbase = row * (size_t)(cols / group);
     const uint32_t nchunks = cols >> 5;
@@ -431,31 +484,38 @@ ORC_FMA_CLONES static void q4_qrow_dot2(const uint8_t* gp, const uint16_t* gs, c
         float ag[4] = {0, 0, 0, 0}, au[4] = {0, 0, 0, 0}, xs[4] = {0, 0, 0, 0}, xs2[4] = {0, 0, 0, 0};
         q4_chunk(gp + rb + 16 * (size_t)c, x + 32 * (size_t)c, ag, xs);
         q4_chunk(up + rb + 16 * (size_t)c, x + 32 * (size_t)c, au, xs2);   /* (xs2 == xs) */
-        const float sg = orc_f16_to_f32(gs[sbase + (c << 5) / group]);
-        const float su = orc_f16_to_f32(us[sbase + (c << 5) / group]);
+        const size_t si = sbase + (c << 5) / group;
         const float X = ((xs[0] + xs[1]) + xs[2]) + xs[3];
-        ga[c & 31u] = fmaf(sg, (((ag[0] + ag[1]) + ag[2]) + ag[3]) * (1.0f / 7.5f) - X, ga[c & 31u]);
-        ua[c & 31u] = fmaf(su, (((au[0] + au[1]) + au[2]) + au[3]) * (1.0f / 7.5f) - X, ua[c & 31u]);
+        const float Ag = ((ag[0] + ag[1]) + ag[2]) + ag[3], Au = ((au[0] + au[1]) + au[2]) + au[3];
+        if (gm) {
+            ga[c & 31u] = fmaf(orc_bf16_to_f32(gs[si]), Ag, fmaf(orc_bf16_to_f32(gm[si]), X, ga[c & 31u]));
+            ua[c & 31u] = fmaf(orc_bf16_to_f32(us[si]), Au, fmaf(orc_bf16_to_f32(um[si]), X, ua[c & 31u]));
+        } else {
+            ga[c & 31u] = fmaf(orc_f16_to_f32(gs[si]), Ag * (1.0f / 7.5f) - X, ga[c & 31u]);
+            ua[c & 31u] = fmaf(orc_f16_to_f32(us[si]), Au * (1.0f / 7.5f) - X, ua[c & 31u]);
+        }
     }
     *g_out = simd_sum32(ga);
     *u_out = simd_sum32(ua);
 }
 
-static void expert_ffn_decode_rows(const uint8_t* pg, const uint16_t* sg, const uint8_t* pu, const uint16_t* su,
-                                   const uint8_t* pd, const uint16_t* sd, const float* x, float* hidden,
-                                   float* out, uint32_t d_ff, uint32_t d_model, uint32_t group, int parallel)
+/* mg/mu/md: NULL for SMOE-Q4, else the mins of the scale+min format */
+static void expert_ffn_decode_rows(const uint8_t* pg, const uint16_t* sg, const uint16_t* mg, const uint8_t* pu,
+                                   const uint16_t* su, const uint16_t* mu, const uint8_t* pd, const uint16_t* sd,
+                                   const uint16_t* md, const float* x, float* hidden, float* out, uint32_t d_ff,
+                                   uint32_t d_model, uint32_t group)
 {
-#pragma omp parallel num_threads(g_threads) if (parallel && g_threads > 1)
+#pragma omp parallel num_threads(g_threads) if (g_threads > 1)
     {
 #pragma omp for schedule(static)
         for (uint32_t r = 0; r < d_ff; ++r) {
             float g, u;
-            q4_qrow_dot2(pg, sg, pu, su, r, d_model, group, x, &g, &u);
+            q4_qrow_dot2(pg, sg, mg, pu, su, mu, r, d_model, group, x, &g, &u);
             hidden[r] = orc_silu(g) * u;                   /* kernels.metal:333-335 */
         }
 #pragma omp for schedule(static)
         for (uint32_t d = 0; d < d_model; ++d)
-            out[d] = q4_qrow_dot(pd, sd, d, d_ff, group, hidden);   /* kernels.metal:360-364 */
+            out[d] = q4_qrow_dot(pd, sd, md, d, d_ff, group, hidden);   /* kernels.metal:360-364 */
     }
 }
 
@@ -463,7 +523,15 @@ void orc_expert_ffn_decode(const uint8_t* pg, const uint16_t* sg, const uint8_t*
                            const uint8_t* pd, const uint16_t* sd, const float* x, float* hidden, float* out,
                            uint32_t d_ff, uint32_t d_model, uint32_t group)
 {
-    expert_ffn_decode_rows(pg, sg, pu, su, pd, sd, x, hidden, out, d_ff, d_model, group, 1);
+    expert_ffn_decode_rows(pg, sg, NULL, pu, su, NULL, pd, sd, NULL, x, hidden, out, d_ff, d_model, group);
+}
+
+void orc_expert_ffn_decode_min(const uint8_t* pg, const uint16_t* sg, const uint16_t* mg, const uint8_t* pu,
+                               const uint16_t* su, const uint16_t* mu, const uint8_t* pd, const uint16_t* sd,
+                               const uint16_t* md, const float* x, float* hidden, float* out, uint32_t d_ff,
+                               uint32_t d_model, uint32_t group)
+{
+    expert_ffn_decode_rows(pg, sg, mg, pu, su, mu, pd, sd, md, x, hidden, out, d_ff, d_model, group);
 }
 
 /* The same FFN with one thread, for callers that already run in parallel. */
@@ -533,7 +601,14 @@ void orc_moe_decode_layer(const OrcShape* s, const OrcLayer* L, float* hidden,
     for (uint32_t e = 0; e < nk; ++e) {                        /* :482-498 */
         const uint8_t *pg, *pu, *pd; const uint16_t *sg, *su, *sd;
         expert_ptrs(L, rid[e], &pg, &sg, &pu, &su, &pd, &sd);
-        orc_expert_ffn_decode(pg, sg, pu, su, pd, sd, normed, h, y, I, D, s->group_size);
+        if (s->quant) {
+            /* scale+min: each matrix's mins follow its D*I/group scales */
+            const size_t ng = (size_t)D * I / s->group_size;
+            orc_expert_ffn_decode_min(pg, sg, sg + ng, pu, su, su + ng, pd, sd, sd + ng, normed, h, y, I, D,
+                                      s->group_size);
+        } else {
+            orc_expert_ffn_decode(pg, sg, pu, su, pd, sd, normed, h, y, I, D, s->group_size);
+        }
         if (expert_out) memcpy(expert_out + (size_t)e * D, y, D * sizeof(float));
         orc_axpy_f32(routed, w[e], y, D);
     }

@@ -111,10 +111,24 @@ void orc_expert_ffn_decode(const uint8_t* pg, const uint16_t* sg,
                            const uint8_t* pd, const uint16_t* sd,
                            const float* x, float* hidden, float* out,
                            uint32_t d_ff, uint32_t d_model, uint32_t group);
+/* the same lanes and chunks for the scale+min format (no counterpart in the
+ * reference): chunk value s * A + m * X, with the mins mg/mu/md */
+void orc_expert_ffn_decode_min(const uint8_t* pg, const uint16_t* sg, const uint16_t* mg,
+                               const uint8_t* pu, const uint16_t* su, const uint16_t* mu,
+                               const uint8_t* pd, const uint16_t* sd, const uint16_t* md,
+                               const float* x, float* hidden, float* out,
+                               uint32_t d_ff, uint32_t d_model, uint32_t group);
+/* ---- the scale+min format (no counterpart in the reference): quantizer and
+ *      per-weight dequant w = code * s + m, bf16 s and m per group ---------- */
+void orc_quantize_q4_min(const float* w, size_t n, uint32_t group, uint8_t* packed,
+                         uint16_t* scales, uint16_t* mins);
+float orc_dequant_q4_min(const uint8_t* packed, const uint16_t* scales, const uint16_t* mins,
+                         size_t wi, uint32_t group);
 
 /* ---- A11: resident expert pool addressing -------------------------------- */
 typedef struct {
     uint32_t d_model, n_experts, top_k, d_ff, group_size, norm_topk;
+    uint32_t quant;   /* 0 SMOE-Q4; 1 the scale+min format (mins after each matrix's scales) */
 } OrcShape;
 
 typedef struct {

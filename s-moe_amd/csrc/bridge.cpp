@@ -835,7 +835,14 @@ static int moe_forward(SmoeMetalCtx* ctx, const SmoeMoeShape* shape, const SmoeM
     const LayerDesc L = layer_of(layer);
     uint32_t* ids = ids_out ? ids_out : s.ids;
     float* w = weights_out ? weights_out : s.w;
-    if (n_tokens == 1 && ctx->decode_engine != SMOE_DECODE_SPLIT && smoe::layer_supported(d, L)) {
+    const bool one_launch = n_tokens == 1 && ctx->decode_engine != SMOE_DECODE_SPLIT && smoe::layer_supported(d, L);
+    if (d.quant != SMOE_QUANT_SMOEQ4 && !one_launch) {
+        std::snprintf(ctx->last_err, sizeof(ctx->last_err),
+                      "the scale+min format runs on the one-launch decode kernel only (one token, top_k 8, "
+                      "<= 128 experts, d_model <= 2048, not under SMOE_DECODE_SPLIT)");
+        return SMOE_ERR_BITS;
+    }
+    if (one_launch) {
         if (!timed(ctx, SMOE_KERNEL_MOE_LAYER, "moe_layer", [&] {
                 return smoe::launch_moe_layer(d, L, hidden, s.lx, ids, w, ctx->d_err, ctx->stream);
             }))
@@ -972,6 +979,7 @@ extern "C" int smoe_hip_moe_prefill(SmoeMetalCtx* ctx, const SmoeMoeShape* shape
     if (!layer->norm_w || !layer->router_w || !layer->experts) return SMOE_ERR_ARG;
     int rc = shape_check(shape);
     if (rc != SMOE_OK) return rc;
+    if (shape->quant != SMOE_QUANT_SMOEQ4) return SMOE_ERR_BITS;   // the grouped GEMMs decode SMOE-Q4 only
     const MoeDims d = dims_of(shape);
     const LayerDesc L = layer_of(layer);
     const uint32_t tmax = prefill_max_tokens(d.E, d.K);
@@ -1081,6 +1089,17 @@ extern "C" int smoe_hip_quantize_q4(SmoeMetalCtx* ctx, const float* w, uint64_t 
                : SMOE_ERR_HIP;
 }
 
+extern "C" int smoe_hip_quantize_q4_scale_min(SmoeMetalCtx* ctx, const float* w, uint64_t n, uint32_t group_size,
+                                              uint8_t* packed, uint16_t* scales, uint16_t* mins)
+{
+    if (!ctx || !w || !packed || !scales || !mins || n == 0) return SMOE_ERR_ARG;
+    if (group_size != 64 || n % group_size) return SMOE_ERR_SHAPE;
+    return hip_ok(ctx, smoe::launch_quantize_q4_min(w, n, group_size, packed, scales, mins, ctx->stream),
+                  "quantize_q4_scale_min")
+               ? SMOE_OK
+               : SMOE_ERR_HIP;
+}
+
 extern "C" int smoe_hip_synth_normal(SmoeMetalCtx* ctx, float* out, uint64_t n, uint64_t seed, uint64_t stream,
                                      float stddev)
 {
@@ -1107,12 +1126,13 @@ extern "C" int smoe_hip_synth_expert_pool(SmoeMetalCtx* ctx, uint8_t* base, uint
     const int rc = shape_check(shape);
     if (rc != SMOE_OK) return rc;
     const uint64_t n = uint64_t(shape->d_model) * shape->d_ff;
-    const uint64_t pb = n / 2, sb = n / shape->group_size * 2;
+    // (scale+min: each matrix's mins follow its scales)
+    const uint64_t pb = n / 2, sb = n / shape->group_size * 2 * (shape->quant == SMOE_QUANT_Q4_SCALE_MIN ? 2 : 1);
     const uint64_t off[6] = {0, pb, pb + sb, 2 * pb + sb, 2 * (pb + sb), 3 * pb + 2 * sb};
     if (expert_stride < 3 * (pb + sb) || expert_stride % 16) return SMOE_ERR_SHAPE;
     return hip_ok(ctx, smoe::launch_synth_pool(base, first_layer, n_layers, n_experts, expert_stride,
                                                shape->d_model, shape->d_ff, shape->group_size, off, seed, stddev,
-                                               ctx->stream),
+                                               shape->quant, ctx->stream),
                   "synth_pool")
                ? SMOE_OK
                : SMOE_ERR_HIP;

@@ -134,7 +134,9 @@ extern "C" int smoe_hip_moe_decode_static(const SmoeMoeShape* shape, const SmoeM
     float* w = weights_out ? weights_out : reinterpret_cast<float*>(base + NA_W);
     uint32_t* err = err_out ? err_out : reinterpret_cast<uint32_t*>(base + NA_ERR);
     hipError_t e;
-    if (smoe::layer_supported(d, L)) {
+    const bool one_launch = smoe::layer_supported(d, L);
+    if (d.quant != SMOE_QUANT_SMOEQ4 && !one_launch) return SMOE_ERR_BITS;   // scale+min: one-launch kernel only
+    if (one_launch) {
         e = smoe::launch_moe_layer(d, L, hidden, base + NA_LX, ids, w, err, s);
     } else {
         float* h = reinterpret_cast<float*>(base + NA_H);

@@ -358,6 +358,7 @@ struct Q4Act {
     uint32_t dig[Q4_DIGITS][4];   // [digit l][dword w]
     float xsum_half;              // X / 2
     float kscale;                 // 2^-sh / 7.5
+    float pscale;                 // 2^-sh
 };
 
 __device__ __forceinline__ void q4_act_from_floats(const float (&a)[32], Q4Act& q)
@@ -385,6 +386,7 @@ __device__ __forceinline__ void q4_act_from_floats(const float (&a)[32], Q4Act& 
     }
     q.xsum_half = 0.5f * static_cast<float>(static_cast<int>(usum - 32u * kB));
     q.kscale = __builtin_ldexpf(1.0f / 7.5f, -sh);
+    q.pscale = __builtin_ldexpf(1.0f, -sh);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         const uint32_t* t = y + 8 * w;
@@ -409,9 +411,8 @@ __device__ __forceinline__ void q4_act_from_floats(const float (&a)[32], Q4Act& 
     }
 }
 
-// sum_k (c_k - 7.5) a_k / 7.5 over one 16-byte chunk of codes (before the
-// group scale)
-__device__ __forceinline__ float q4_chunk_dot8(uint4 v, const Q4Act& q)
+// sum_k (c_k - 8) t_k over one 16-byte chunk of codes, exact
+__device__ __forceinline__ int q4_chunk_int(uint4 v, const Q4Act& q)
 {
     // c ^ 8 per nibble is c - 8 as a two's-complement nibble
     const uint32_t c[4] = {v.x ^ 0x88888888u, v.y ^ 0x88888888u, v.z ^ 0x88888888u, v.w ^ 0x88888888u};
@@ -426,7 +427,24 @@ __device__ __forceinline__ float q4_chunk_dot8(uint4 v, const Q4Act& q)
     uint32_t acc = static_cast<uint32_t>(s[Q4_DIGITS - 1]);
 #pragma unroll
     for (int l = Q4_DIGITS - 2; l >= 0; --l) acc = acc * 16u + static_cast<uint32_t>(s[l]);
-    return (static_cast<float>(static_cast<int>(acc)) + q.xsum_half) * q.kscale;
+    return static_cast<int>(acc);
+}
+
+// sum_k (c_k - 7.5) a_k / 7.5 over one 16-byte chunk of codes (before the
+// group scale)
+__device__ __forceinline__ float q4_chunk_dot8(uint4 v, const Q4Act& q)
+{
+    return (static_cast<float>(q4_chunk_int(v, q)) + q.xsum_half) * q.kscale;
+}
+
+// sum_k (c_k s + m) a_k over one chunk of the scale+min format (scale s and
+// min m of the chunk's group): c s + m = (c - 8) s + (m + 8 s), so the
+// exact integer sum_k (c_k - 8) t_k and X = sum_k t_k carry it without
+// cancelling the min against the codes
+__device__ __forceinline__ float q4_chunk_affine(uint4 v, const Q4Act& q, float s, float m)
+{
+    const float b = fmaf(8.0f, s, m);
+    return fmaf(s, static_cast<float>(q4_chunk_int(v, q)), b * (2.0f * q.xsum_half)) * q.pscale;
 }
 
 // Per-chunk affine epilogue of the dequant w = (c - 7.5) * (1/7.5) * s:

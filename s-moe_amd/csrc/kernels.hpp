@@ -60,6 +60,7 @@ struct ExpertPtrs {
 
 struct MoeDims {
     uint32_t D, E, K, I, group, norm_topk;
+    uint32_t quant = 0;   // SMOE_QUANT_*: 0 fp16 absmax (SMOE-Q4), 1 bf16 scale + bf16 min
 };
 
 struct LayerDesc {
@@ -255,9 +256,14 @@ hipError_t launch_synth_bf16(uint16_t* out, uint64_t n, uint64_t seed, uint64_t 
                              float stddev, hipStream_t s);
 hipError_t launch_quantize_q4(const float* w, uint64_t n, uint32_t group, uint8_t* packed,
                               uint16_t* scales, hipStream_t s);
+// the scale+min format: scales and mins [n / group] bf16 bits
+hipError_t launch_quantize_q4_min(const float* w, uint64_t n, uint32_t group, uint8_t* packed,
+                                  uint16_t* scales, uint16_t* mins, hipStream_t s);
+// quant: SMOE_QUANT_*; with the scale+min format each matrix's mins follow
+// its D*I/group scales
 hipError_t launch_synth_pool(uint8_t* base, uint32_t first_layer, uint32_t n_layers,
                              uint32_t n_experts, uint64_t stride, uint32_t D, uint32_t I,
                              uint32_t group, const uint64_t* off6, uint64_t seed,
-                             float stddev, hipStream_t s);
+                             float stddev, uint32_t quant, hipStream_t s);
 
 }  // namespace smoe

@@ -122,7 +122,10 @@ __device__ __forceinline__ bool give_up(uint32_t spins, const LayerIO& io)
 // one copy of the hidden state and norm weights and one of the XCD's h in
 // LDS (the CU then reads them from the L2 once instead of once per wave); the
 // whole block calls the step.
-template <int CPL, int VPL, int SEG, int DR, int RB, int NW, bool CHAIN>
+// QF: the group format (0 SMOE-Q4: fp16 scale s, w = (c - 7.5) / 7.5 s; 1 the
+// scale+min format: bf16 scale s and min m after all scales of the matrix,
+// w = c s + m; GATHER configurations only).
+template <int CPL, int VPL, int SEG, int DR, int RB, int NW, bool CHAIN, int QF>
 __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc& L, const LayerIO& io,
                                                uint64_t* __restrict__ lx, uint32_t tag, uint32_t* ids_out,
                                                float* w_out, uint32_t n_up, uint32_t n_down, uint32_t t, uint32_t x,
@@ -371,6 +374,9 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     // wide configurations load each lane's scale beside its row piece (the
     // LDS hand-over costs the 235B layer 2.8 us).
     constexpr bool GATHER = PROPOSE && CPL == 1;
+    static_assert(QF == 0 || GATHER, "the scale+min format runs on the gathered-scale configurations");
+    // (scale+min: a matrix's mins start D * I / 64 entries after its scales)
+    const size_t min_bytes = QF ? static_cast<size_t>(D) * d.I / 32 : 0;
     // DFIRST (the same, narrow configurations with 16 down rows a wave, in
     // the chain): the down rows are requested first, ahead of the gate/up
     // rows, so that they have landed when h is published and polled (loads
@@ -382,10 +388,11 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     constexpr int NSD = GATHER ? (RW * DN_MAX_I / 512 + WAVE - 1) / WAVE : 1;   // down scale pieces per lane
     const uint32_t nsq_up = RB * D / 512, nsq_dn = RW * d.I / 512;
     uint4 va[RB][CPL], vb[RB][CPL], qa_s, qb_s, qd_s[NSD];
+    uint4 qa_m, qb_m, qd_m[QF ? NSD : 1];
     uint16_t sva[GATHER ? 1 : RB][CPL], svb[GATHER ? 1 : RB][CPL], dsv[GATHER ? 1 : DR];
     uint4 dv[DR];
-    __shared__ uint4 sc_up_all[NW][GATHER ? 2 : 1][WAVE];
-    __shared__ uint4 sc_dn_all[NW][NSD * WAVE];
+    __shared__ uint4 sc_up_all[NW][GATHER ? (QF ? 4 : 2) : 1][WAVE];
+    __shared__ uint4 sc_dn_all[NW][(QF ? 2 : 1) * NSD * WAVE];
     auto& sc_up = sc_up_all[wv];
     auto& sc_dn = sc_dn_all[wv];
     auto issue_up = [&](const uint8_t* blob) {
@@ -397,6 +404,10 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
             const uint32_t q = min(static_cast<uint32_t>(lane), nsq_up - 1);
             qa_s = load_stream_u4(blob + L.off[1] + static_cast<size_t>(rowg) * row_scales * 2 + q * 16);
             qb_s = load_stream_u4(blob + L.off[3] + static_cast<size_t>(rowg) * row_scales * 2 + q * 16);
+            if constexpr (QF) {
+                qa_m = load_stream_u4(blob + L.off[1] + min_bytes + static_cast<size_t>(rowg) * row_scales * 2 + q * 16);
+                qb_m = load_stream_u4(blob + L.off[3] + min_bytes + static_cast<size_t>(rowg) * row_scales * 2 + q * 16);
+            }
         }
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
@@ -422,6 +433,9 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
             for (int k = 0; k < NSD; ++k) {
                 const uint32_t q = min(static_cast<uint32_t>(k * WAVE + lane), nsq_dn - 1);
                 qd_s[k] = load_stream_u4(blob + L.off[5] + static_cast<size_t>(t) * RW * (d.I / 32) + q * 16);
+                if constexpr (QF)
+                    qd_m[k] = load_stream_u4(blob + L.off[5] + min_bytes + static_cast<size_t>(t) * RW * (d.I / 32) +
+                                             q * 16);
             }
         }
 #pragma unroll
@@ -474,10 +488,16 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
         if constexpr (GATHER) {
             sc_up[0][lane] = qa_s;
             sc_up[GATHER ? 1 : 0][lane] = qb_s;
+            if constexpr (QF) {
+                sc_up[QF ? 2 : 0][lane] = qa_m;
+                sc_up[QF ? 3 : 0][lane] = qb_m;
+            }
             __builtin_amdgcn_wave_barrier();
         }
         const uint16_t* sga = reinterpret_cast<const uint16_t*>(sc_up[0]);
         const uint16_t* sgb = reinterpret_cast<const uint16_t*>(sc_up[GATHER ? 1 : 0]);
+        const uint16_t* mga = reinterpret_cast<const uint16_t*>(sc_up[QF ? 2 : 0]);
+        const uint16_t* mgb = reinterpret_cast<const uint16_t*>(sc_up[QF ? 3 : 0]);
         float part[NR];
 #pragma unroll
         for (int i = 2 * RB; i < NR; ++i) part[i] = 0.f;
@@ -489,8 +509,13 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
                 const uint32_t si = i * row_scales + (min(lane + WAVE * j, nch - 1) * 32) / LX_GROUP;
                 const uint16_t s_a = GATHER ? sga[si] : sva[GATHER ? 0 : i][j];
                 const uint16_t s_b = GATHER ? sgb[si] : svb[GATHER ? 0 : i][j];
-                ga = fmaf(f16_bits_to_f32(s_a), q4_chunk_dot8(va[i][j], qa[j]), ga);
-                ua = fmaf(f16_bits_to_f32(s_b), q4_chunk_dot8(vb[i][j], qa[j]), ua);
+                if constexpr (QF) {
+                    ga += q4_chunk_affine(va[i][j], qa[j], bf16_to_f32(s_a), bf16_to_f32(mga[si]));
+                    ua += q4_chunk_affine(vb[i][j], qa[j], bf16_to_f32(s_b), bf16_to_f32(mgb[si]));
+                } else {
+                    ga = fmaf(f16_bits_to_f32(s_a), q4_chunk_dot8(va[i][j], qa[j]), ga);
+                    ua = fmaf(f16_bits_to_f32(s_b), q4_chunk_dot8(vb[i][j], qa[j]), ua);
+                }
             }
             part[2 * i] = ga;
             part[2 * i + 1] = ua;
@@ -606,14 +631,23 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
         if constexpr (GATHER) {
 #pragma unroll
             for (int k = 0; k < NSD; ++k) sc_dn[k * WAVE + lane] = qd_s[k];
+            if constexpr (QF) {
+#pragma unroll
+                for (int k = 0; k < NSD; ++k) sc_dn[(NSD + k) * WAVE + lane] = qd_m[QF ? k : 0];
+            }
             __builtin_amdgcn_wave_barrier();
         }
         const uint16_t* sd = reinterpret_cast<const uint16_t*>(sc_dn);
+        const uint16_t* sdm = reinterpret_cast<const uint16_t*>(sc_dn + (QF ? NSD * WAVE : 0));
         float acc[DR];
 #pragma unroll
         for (int i = 0; i < DR; ++i) {
             const uint32_t si = (static_cast<uint32_t>(gi) * DR + i) * (d.I / LX_GROUP) + (dc * 32) / LX_GROUP;
-            const float y = f16_bits_to_f32(GATHER ? sd[si] : dsv[GATHER ? 0 : i]) * q4_chunk_dot8(dv[i], qh);
+            float y;
+            if constexpr (QF)
+                y = q4_chunk_affine(dv[i], qh, bf16_to_f32(sd[si]), bf16_to_f32(sdm[si]));
+            else
+                y = f16_bits_to_f32(GATHER ? sd[si] : dsv[GATHER ? 0 : i]) * q4_chunk_dot8(dv[i], qh);
             acc[i] = act ? y : 0.f;
         }
         // lane l holds the total of row (l >> SH) & (DR - 1) of group l >> SEG
@@ -670,7 +704,7 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
 
 // Blocks of NW waves; block b is the (b / 8)-th of its XCD, its wave w has
 // t = NW (b / 8) + w.
-template <int CPL, int VPL, int SEG, int DR, int RB, int NW>
+template <int CPL, int VPL, int SEG, int DR, int RB, int NW, int QF>
 __global__ __launch_bounds__(NW * WAVE)
 void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* __restrict__ lx,
                  uint32_t* __restrict__ ids_out, float* __restrict__ w_out, uint32_t n_up, uint32_t n_down,
@@ -686,7 +720,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
     io.hout = hidden;
     io.py = lx + LX_HEAD + 8u * lx_pad(d.E) + 8u * lx_pad(d.I);
     const bool to =
-        moe_layer_step<CPL, VPL, SEG, DR, RB, NW, false>(d, L, io, lx, tag, ids_out, w_out, n_up, n_down, t, x, nbx);
+        moe_layer_step<CPL, VPL, SEG, DR, RB, NW, false, QF>(d, L, io, lx, tag, ids_out, w_out, n_up, n_down, t, x, nbx);
     // the combiner of row block 0 on XCD 0 advances the epoch
     if (x == 0 && t == 0 && t < n_down) {
         __builtin_amdgcn_wave_barrier();
@@ -707,7 +741,7 @@ void k_moe_layer(MoeDims d, LayerDesc L, float* __restrict__ hidden, uint64_t* _
 // layer l + 1's partials while another XCD still reads layer l's, never layer
 // l - 1's: that needs every XCD's layer l partials).  A wave that times out
 // stores the abort word, after which every wait of the launch ends.
-template <int CPL, int VPL, int SEG, int DR, int RB, int NW>
+template <int CPL, int VPL, int SEG, int DR, int RB, int NW, int QF>
 __global__ __launch_bounds__(NW * WAVE)
 void k_moe_chain(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_layers, float* __restrict__ hidden,
                  uint64_t* __restrict__ lx, float* __restrict__ hcopy, uint32_t* __restrict__ cnt,
@@ -739,7 +773,7 @@ void k_moe_chain(MoeDims d, const LayerDesc* __restrict__ layers, uint32_t n_lay
         io.abort = cnt + 8 * CHAIN_FLAGS;
         io.abort_val = tag_at(ep0, 0);
         io.next_router = last ? nullptr : layers[l + 1].router_w;
-        to |= moe_layer_step<CPL, VPL, SEG, DR, RB, NW, true>(d, L, io, lx, tag, ids_out + l * d.K,
+        to |= moe_layer_step<CPL, VPL, SEG, DR, RB, NW, true, QF>(d, L, io, lx, tag, ids_out + l * d.K,
                                                                w_out + l * d.K, n_up, n_down, t, x, nbx);
     }
     // wave 0 of XCD 0 advances the epoch once its last combine is done (that
@@ -767,23 +801,23 @@ struct LayerCfg {
 // kernel keeps one-wave blocks, 1 % faster there).
 constexpr bool shares_loads(int cpl, int seg) { return (cpl == 2 && seg == 6) || (cpl == 1 && seg == 5); }
 
-template <int CPL, int VPL, int SEG, int DR, int RB, bool CHAIN, int NW>
+template <int CPL, int VPL, int SEG, int DR, int RB, bool CHAIN, int NW, int QF>
 auto kernel_of()
 {
-    if constexpr (CHAIN) return k_moe_chain<CPL, VPL, SEG, DR, RB, NW>;
-    else return k_moe_layer<CPL, VPL, SEG, DR, RB, NW>;
+    if constexpr (CHAIN) return k_moe_chain<CPL, VPL, SEG, DR, RB, NW, QF>;
+    else return k_moe_layer<CPL, VPL, SEG, DR, RB, NW, QF>;
 }
 
 // Dynamic LDS added to a block of NW > 1 waves so that only one fits on a CU
 // (its waves then have the CU's memory path to themselves, as the one-wave
 // blocks of a grid spread four or six to a CU do).
-template <int CPL, int VPL, int SEG, int DR, int RB, bool CHAIN, int NW>
+template <int CPL, int VPL, int SEG, int DR, int RB, bool CHAIN, int NW, int QF>
 uint32_t lds_pad()
 {
     static uint32_t pad = [] {
         if (NW == 1) return 0u;
         hipFuncAttributes attr{};
-        if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel_of<CPL, VPL, SEG, DR, RB, CHAIN, NW>())) !=
+        if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kernel_of<CPL, VPL, SEG, DR, RB, CHAIN, NW, QF>())) !=
             hipSuccess)
             return 0u;
         const size_t want = 82u * 1024u;
@@ -792,15 +826,15 @@ uint32_t lds_pad()
     return pad;
 }
 
-template <int CPL, int VPL, int SEG, int DR, int RB, bool CHAIN, int NW>
+template <int CPL, int VPL, int SEG, int DR, int RB, bool CHAIN, int NW, int QF>
 uint32_t resident_blocks()
 {
     static uint32_t cap = [] {
         int dev = 0, per_cu = 0, cus = 0;
         if (hipGetDevice(&dev) != hipSuccess) return 0u;
         if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0u;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel_of<CPL, VPL, SEG, DR, RB, CHAIN, NW>(),
-                                                         NW * WAVE, lds_pad<CPL, VPL, SEG, DR, RB, CHAIN, NW>()) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel_of<CPL, VPL, SEG, DR, RB, CHAIN, NW, QF>(),
+                                                         NW * WAVE, lds_pad<CPL, VPL, SEG, DR, RB, CHAIN, NW, QF>()) !=
             hipSuccess)
             return 0u;
         return static_cast<uint32_t>(per_cu) * static_cast<uint32_t>(cus);
@@ -816,6 +850,8 @@ bool layer_cfg(const MoeDims& d, LayerCfg& c)
     c.cpl = nch <= 64 ? 1 : nch <= 128 ? 2 : 0;
     if (!c.cpl) return false;
     c.vpl = d.E <= 128 ? 2 : 8;
+    // the scale+min format: the gathered-scale (narrow, proposing) configurations
+    if (d.quant != 0 && (c.cpl != 1 || c.vpl != 2)) return false;
     const uint32_t ch = d.I / 32;
     if (ch <= 32) {
         c.seg = 5;
@@ -859,51 +895,59 @@ struct LaunchArgs {
     uint32_t* err = nullptr;
 };
 
-template <int CPL, int VPL, int SEG, int DR, int RB, bool CHAIN, int NW>
+template <int CPL, int VPL, int SEG, int DR, int RB, bool CHAIN, int NW, int QF>
 hipError_t launch_nw(const LayerCfg& c, const MoeDims& d, const LaunchArgs& a, hipStream_t s, bool dry)
 {
     const uint32_t blocks = 8u * c.nbx / NW;
-    if (blocks > resident_blocks<CPL, VPL, SEG, DR, RB, CHAIN, NW>() || (CHAIN && c.n_down > CHAIN_FLAGS))
+    if (blocks > resident_blocks<CPL, VPL, SEG, DR, RB, CHAIN, NW, QF>() || (CHAIN && c.n_down > CHAIN_FLAGS))
         return hipErrorInvalidConfiguration;
     if (dry) return hipSuccess;
-    const uint32_t pad = lds_pad<CPL, VPL, SEG, DR, RB, CHAIN, NW>();
+    const uint32_t pad = lds_pad<CPL, VPL, SEG, DR, RB, CHAIN, NW, QF>();
     if constexpr (CHAIN)
-        launch_kernel_lds(k_moe_chain<CPL, VPL, SEG, DR, RB, NW>, dim3(blocks), dim3(NW * WAVE), pad, s, d, a.layers,
-                          a.n_layers, a.hidden, a.lx, a.hcopy, a.cnt, a.ids, a.w, c.n_up, c.n_down, a.err);
+        launch_kernel_lds(k_moe_chain<CPL, VPL, SEG, DR, RB, NW, QF>, dim3(blocks), dim3(NW * WAVE), pad, s, d,
+                          a.layers, a.n_layers, a.hidden, a.lx, a.hcopy, a.cnt, a.ids, a.w, c.n_up, c.n_down, a.err);
     else
-        launch_kernel_lds(k_moe_layer<CPL, VPL, SEG, DR, RB, NW>, dim3(blocks), dim3(NW * WAVE), pad, s, d, *a.L,
+        launch_kernel_lds(k_moe_layer<CPL, VPL, SEG, DR, RB, NW, QF>, dim3(blocks), dim3(NW * WAVE), pad, s, d, *a.L,
                           a.hidden, a.lx, a.ids, a.w, c.n_up, c.n_down, a.err);
     return hipGetLastError();
 }
 
-template <int CPL, int VPL, int SEG, int DR, int RB>
+template <int CPL, int VPL, int SEG, int DR, int RB, int QF>
 hipError_t launch_cfg(const LayerCfg& c, const MoeDims& d, const LaunchArgs& a, bool chain, hipStream_t s, bool dry)
 {
     if constexpr (shares_loads(CPL, SEG) && CPL == 1) {
-        if (chain && c.nbx % 4 == 0) return launch_nw<CPL, VPL, SEG, DR, RB, true, 4>(c, d, a, s, dry);
+        if (chain && c.nbx % 4 == 0) return launch_nw<CPL, VPL, SEG, DR, RB, true, 4, QF>(c, d, a, s, dry);
     } else if constexpr (shares_loads(CPL, SEG)) {
         // a block of shared loads where the grid divides into them (one per CU:
         // 256 or 192 waves an XCD)
         if (c.nbx % 8 == 0)
-            return chain ? launch_nw<CPL, VPL, SEG, DR, RB, true, 8>(c, d, a, s, dry)
-                         : launch_nw<CPL, VPL, SEG, DR, RB, false, 8>(c, d, a, s, dry);
+            return chain ? launch_nw<CPL, VPL, SEG, DR, RB, true, 8, QF>(c, d, a, s, dry)
+                         : launch_nw<CPL, VPL, SEG, DR, RB, false, 8, QF>(c, d, a, s, dry);
         if (c.nbx % 6 == 0)
-            return chain ? launch_nw<CPL, VPL, SEG, DR, RB, true, 6>(c, d, a, s, dry)
-                         : launch_nw<CPL, VPL, SEG, DR, RB, false, 6>(c, d, a, s, dry);
+            return chain ? launch_nw<CPL, VPL, SEG, DR, RB, true, 6, QF>(c, d, a, s, dry)
+                         : launch_nw<CPL, VPL, SEG, DR, RB, false, 6, QF>(c, d, a, s, dry);
     }
-    return chain ? launch_nw<CPL, VPL, SEG, DR, RB, true, 1>(c, d, a, s, dry)
-                 : launch_nw<CPL, VPL, SEG, DR, RB, false, 1>(c, d, a, s, dry);
+    return chain ? launch_nw<CPL, VPL, SEG, DR, RB, true, 1, QF>(c, d, a, s, dry)
+                 : launch_nw<CPL, VPL, SEG, DR, RB, false, 1, QF>(c, d, a, s, dry);
 }
 
 hipError_t dispatch(const MoeDims& d, const LaunchArgs& a, bool chain, hipStream_t s, bool dry)
 {
     LayerCfg c;
     if (!layer_cfg(d, c)) return hipErrorInvalidValue;
-#define SMOE_LAYER_CASE(C, V, S, R)                                                           \
+#define SMOE_LAYER_CASE_Q(C, V, S, R, Q)                                                      \
     if (c.cpl == C && c.vpl == V && c.seg == S && c.dr == R && c.rb == 8)                     \
-        return launch_cfg<C, V, S, R, 8>(c, d, a, chain, s, dry);                             \
+        return launch_cfg<C, V, S, R, 8, Q>(c, d, a, chain, s, dry);                          \
     if (c.cpl == C && c.vpl == V && c.seg == S && c.dr == R && c.rb == 6)                     \
-        return launch_cfg<C, V, S, R, 6>(c, d, a, chain, s, dry);
+        return launch_cfg<C, V, S, R, 6, Q>(c, d, a, chain, s, dry);
+#define SMOE_LAYER_CASE(C, V, S, R) SMOE_LAYER_CASE_Q(C, V, S, R, 0)
+    if (d.quant != 0) {
+        // the scale+min format (layer_cfg admits the narrow configurations only)
+        SMOE_LAYER_CASE_Q(1, 2, 5, 8, 1)
+        SMOE_LAYER_CASE_Q(1, 2, 6, 16, 1)
+        SMOE_LAYER_CASE_Q(1, 2, 6, 32, 1)
+        return hipErrorInvalidValue;
+    }
     SMOE_LAYER_CASE(1, 2, 5, 8)
     SMOE_LAYER_CASE(1, 2, 6, 16)
     SMOE_LAYER_CASE(1, 2, 6, 32)
@@ -917,6 +961,7 @@ hipError_t dispatch(const MoeDims& d, const LaunchArgs& a, bool chain, hipStream
     SMOE_LAYER_CASE(2, 8, 6, 16)
     SMOE_LAYER_CASE(2, 8, 6, 32)
 #undef SMOE_LAYER_CASE
+#undef SMOE_LAYER_CASE_Q
     return hipErrorInvalidValue;
 }
 

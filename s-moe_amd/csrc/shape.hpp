@@ -7,13 +7,15 @@
 
 namespace smoe {
 
-// An SmoeMoeShape the decode and prefill kernels accept: SMOE-Q4, group 64
+// An SmoeMoeShape the decode and prefill kernels accept: 4 bits (SMOE-Q4, or
+// the scale+min format where an entry point takes it), group 64
 // (the vault format's group, shatter_moe.py Q2_GROUP_SIZE), d_model and d_ff
 // multiples of 64 up to SMOE_MAX_DIM, top_k <= min(SMOE_MAX_ACTIVE, n_experts).
 inline int shape_check(const SmoeMoeShape* s)
 {
     if (!s) return SMOE_ERR_ARG;
     if (s->bits != 4) return SMOE_ERR_BITS;
+    if (s->quant != SMOE_QUANT_SMOEQ4 && s->quant != SMOE_QUANT_Q4_SCALE_MIN) return SMOE_ERR_BITS;
     const uint32_t g = s->group_size;
     if (g == 0 || g % 32 != 0 || g > 128 || (g & (g - 1))) return SMOE_ERR_SHAPE;
     if (s->d_model == 0 || s->d_ff == 0 || s->n_experts == 0 || s->top_k == 0) return SMOE_ERR_SHAPE;
@@ -28,7 +30,7 @@ inline int shape_check(const SmoeMoeShape* s)
 
 inline MoeDims dims_of(const SmoeMoeShape* s)
 {
-    return MoeDims{s->d_model, s->n_experts, s->top_k, s->d_ff, s->group_size, s->norm_topk ? 1u : 0u};
+    return MoeDims{s->d_model, s->n_experts, s->top_k, s->d_ff, s->group_size, s->norm_topk ? 1u : 0u, s->quant};
 }
 
 inline LayerDesc layer_of(const SmoeMoeLayer* L)

@@ -9,6 +9,9 @@
 // k_quantize_q4 restates quantize_smoeq4 (scripts/shatter_moe.py:331-368):
 // absmax per group of 64 (0 -> 1.0), code = clip(rint(w/absmax*7.5 + 7.5),
 // 0, 15) with round-half-even, fp16(absmax) scale, low nibble = even index.
+// k_quantize_q4_min is this build's scale+min format (no counterpart in the
+// reference): m = bf16(min), s = bf16((max - min) / 15) (bf16 1.0 if that is
+// 0), code = clip(rint((w - m) / s), 0, 15) from the rounded s and m.
 #include "device_common.hpp"
 #include "kernels.hpp"
 
@@ -147,6 +150,42 @@ __device__ __forceinline__ void quantize_group(const float (&w)[G], uint8_t* pac
     for (int q = 0; q < G / 32; ++q) dst[q] = make_uint4(words[4 * q], words[4 * q + 1], words[4 * q + 2], words[4 * q + 3]);
 }
 
+// quantize one group of G weights to the scale+min format
+template <int G>
+__device__ __forceinline__ void quantize_group_min(const float (&w)[G], uint8_t* packed, uint16_t* scale,
+                                                   uint16_t* minv)
+{
+    float lo = w[0], hi = w[0];
+#pragma unroll
+    for (int j = 1; j < G; ++j) {
+        lo = w[j] < lo ? w[j] : lo;
+        hi = w[j] > hi ? w[j] : hi;
+    }
+    const float span = (hi - lo) / 15.0f;
+    uint16_t sb = f32_to_bf16_rne(span);
+    if ((sb & 0x7FFFu) == 0) sb = 0x3F80u;                 // a constant group: s = 1
+    const uint16_t mb = f32_to_bf16_rne(lo);
+    *scale = sb;
+    *minv = mb;
+    const float s = __uint_as_float(static_cast<uint32_t>(sb) << 16);
+    const float m = __uint_as_float(static_cast<uint32_t>(mb) << 16);
+    uint32_t words[G / 8];
+#pragma unroll
+    for (int q = 0; q < G / 8; ++q) words[q] = 0;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        // two separately rounded operations: (w - m), then / s
+        float q = w[j] - m;
+        q = q / s;
+        int c = static_cast<int>(rintf(q));
+        c = c < 0 ? 0 : (c > 15 ? 15 : c);
+        words[j / 8] |= static_cast<uint32_t>(c) << (4 * (j % 8));
+    }
+    uint4* dst = reinterpret_cast<uint4*>(packed);
+#pragma unroll
+    for (int q = 0; q < G / 32; ++q) dst[q] = make_uint4(words[4 * q], words[4 * q + 1], words[4 * q + 2], words[4 * q + 3]);
+}
+
 __global__ void k_synth_normal(float* out, uint64_t n, uint64_t key, float stddev)
 {
     for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
@@ -171,9 +210,22 @@ __global__ void k_quantize_q4(const float* __restrict__ w, uint64_t n_groups, ui
     }
 }
 
-// Expert pool: groups are enumerated as (layer, expert, matrix, group); the
-// three matrices of a blob hold the same number of groups (D*I/G).
 template <int G>
+__global__ void k_quantize_q4_min(const float* __restrict__ w, uint64_t n_groups, uint8_t* __restrict__ packed,
+                                  uint16_t* __restrict__ scales, uint16_t* __restrict__ mins)
+{
+    for (uint64_t g = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; g < n_groups; g += (uint64_t)gridDim.x * blockDim.x) {
+        float v[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) v[j] = w[g * G + j];
+        quantize_group_min<G>(v, packed + g * (G / 2), scales + g, mins + g);
+    }
+}
+
+// Expert pool: groups are enumerated as (layer, expert, matrix, group); the
+// three matrices of a blob hold the same number of groups (D*I/G).  QM: the
+// scale+min format, each matrix's mins right after its scales.
+template <int G, bool QM>
 __global__ void k_synth_pool(uint8_t* base, uint32_t first_layer, uint32_t n_layers, uint32_t n_experts,
                              uint64_t stride, uint64_t groups_per_matrix, uint64_t off0, uint64_t off1,
                              uint64_t off2, uint64_t off3, uint64_t off4, uint64_t off5, uint64_t seed,
@@ -195,7 +247,11 @@ __global__ void k_synth_pool(uint8_t* base, uint32_t first_layer, uint32_t n_lay
         uint8_t* blob = base + le * stride;
         const uint64_t po = m == 0 ? off0 : (m == 1 ? off2 : off4);
         const uint64_t so = m == 0 ? off1 : (m == 1 ? off3 : off5);
-        quantize_group<G>(v, blob + po + g * (G / 2), reinterpret_cast<uint16_t*>(blob + so) + g);
+        uint16_t* sc = reinterpret_cast<uint16_t*>(blob + so) + g;
+        if constexpr (QM)
+            quantize_group_min<G>(v, blob + po + g * (G / 2), sc, sc + groups_per_matrix);
+        else
+            quantize_group<G>(v, blob + po + g * (G / 2), sc);
     }
 }
 
@@ -232,25 +288,35 @@ hipError_t launch_quantize_q4(const float* w, uint64_t n, uint32_t group, uint8_
     return hipGetLastError();
 }
 
+hipError_t launch_quantize_q4_min(const float* w, uint64_t n, uint32_t group, uint8_t* packed, uint16_t* scales,
+                                  uint16_t* mins, hipStream_t s)
+{
+    const uint64_t ng = n / group;
+    if (group != 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_quantize_q4_min<64>, grid_for(ng, 128), dim3(128), 0, s, w, ng, packed, scales, mins);
+    return hipGetLastError();
+}
+
+template <int G>
+static void synth_pool_g(uint8_t* base, uint32_t first_layer, uint32_t n_layers, uint32_t n_experts, uint64_t stride,
+                         uint64_t gpm, const uint64_t* off, uint64_t seed, float stddev, bool qm, hipStream_t s)
+{
+    const uint64_t total = static_cast<uint64_t>(n_layers) * n_experts * 3 * gpm;
+    auto k = qm ? k_synth_pool<G, true> : k_synth_pool<G, false>;
+    hipLaunchKernelGGL(k, grid_for(total, 128), dim3(128), 0, s, base, first_layer, n_layers, n_experts, stride, gpm,
+                       off[0], off[1], off[2], off[3], off[4], off[5], seed, stddev);
+}
+
 hipError_t launch_synth_pool(uint8_t* base, uint32_t first_layer, uint32_t n_layers, uint32_t n_experts,
                              uint64_t stride, uint32_t D, uint32_t I, uint32_t group, const uint64_t* off,
-                             uint64_t seed, float stddev, hipStream_t s)
+                             uint64_t seed, float stddev, uint32_t quant, hipStream_t s)
 {
     const uint64_t gpm = static_cast<uint64_t>(D) * I / group;
-    const uint64_t total = static_cast<uint64_t>(n_layers) * n_experts * 3 * gpm;
+    const bool qm = quant == 1;
     switch (group) {
-        case 32:
-            hipLaunchKernelGGL(k_synth_pool<32>, grid_for(total, 128), dim3(128), 0, s, base, first_layer, n_layers,
-                               n_experts, stride, gpm, off[0], off[1], off[2], off[3], off[4], off[5], seed, stddev);
-            break;
-        case 64:
-            hipLaunchKernelGGL(k_synth_pool<64>, grid_for(total, 128), dim3(128), 0, s, base, first_layer, n_layers,
-                               n_experts, stride, gpm, off[0], off[1], off[2], off[3], off[4], off[5], seed, stddev);
-            break;
-        case 128:
-            hipLaunchKernelGGL(k_synth_pool<128>, grid_for(total, 128), dim3(128), 0, s, base, first_layer, n_layers,
-                               n_experts, stride, gpm, off[0], off[1], off[2], off[3], off[4], off[5], seed, stddev);
-            break;
+        case 32: synth_pool_g<32>(base, first_layer, n_layers, n_experts, stride, gpm, off, seed, stddev, qm, s); break;
+        case 64: synth_pool_g<64>(base, first_layer, n_layers, n_experts, stride, gpm, off, seed, stddev, qm, s); break;
+        case 128: synth_pool_g<128>(base, first_layer, n_layers, n_experts, stride, gpm, off, seed, stddev, qm, s); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

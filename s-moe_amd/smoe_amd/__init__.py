@@ -45,7 +45,10 @@ def hidden_stream(index: int) -> int:
 
 class SmoeMoeShape(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in
-                ("d_model", "n_experts", "top_k", "d_ff", "group_size", "bits", "norm_topk")]
+                ("d_model", "n_experts", "top_k", "d_ff", "group_size", "bits", "norm_topk", "quant")]
+
+
+QUANT_SMOEQ4, QUANT_Q4_SCALE_MIN = 0, 1
 
 
 class SmoeMoeLayer(C.Structure):
@@ -113,6 +116,7 @@ SIGNATURES = [
     ("smoe_hip_compute_top_k", _I, [_VP, _VP, _U32, _U32, _U32, _VP, _VP, _I]),
     ("smoe_hip_permute", _I, [_VP, _VP, _VP, _U32, _U32, _U32, _VP, _VP, _VP, _VP, _VP]),
     ("smoe_hip_quantize_q4", _I, [_VP, _VP, _U64, _U32, _VP, _VP]),
+    ("smoe_hip_quantize_q4_scale_min", _I, [_VP, _VP, _U64, _U32, _VP, _VP, _VP]),
     ("smoe_hip_synth_normal", _I, [_VP, _VP, _U64, _U64, _U64, _F]),
     ("smoe_hip_synth_bf16", _I, [_VP, _VP, _U64, _U64, _U64, _F]),
     ("smoe_hip_synth_expert_pool", _I, [_VP, _VP, _U32, _U32, _U32, _U64, _SHP, _U64, _F]),
@@ -164,22 +168,28 @@ def lib():
 
 
 class SmoeError(RuntimeError):
-    pass
+    """A non-zero status of the C ABI; `code` is the SMOE_ERR_* value."""
+
+    def __init__(self, msg, code=None):
+        super().__init__(msg)
+        self.code = code
 
 
-def blob_layout(d_model: int, d_ff: int, group: int = 64):
+def blob_layout(d_model: int, d_ff: int, group: int = 64, quant: int = 0):
     """Offsets of the six tensors in one expert blob (build_expert_blob,
-    shatter_moe.py:627-674), the raw blob size and the 16 KB-padded stride."""
+    shatter_moe.py:627-674), the raw blob size and the 16 KB-padded stride.
+    quant=QUANT_Q4_SCALE_MIN: each matrix's bf16 mins follow its bf16 scales
+    inside the scales' region (twice the SMOE-Q4 size)."""
     n = d_model * d_ff
-    pb, sb = n // 2, n // group * 2
+    pb, sb = n // 2, n // group * 2 * (2 if quant == QUANT_Q4_SCALE_MIN else 1)
     off = [0, pb, pb + sb, 2 * pb + sb, 2 * (pb + sb), 3 * pb + 2 * sb]
     raw = 3 * (pb + sb)
     stride = (raw + PAGE - 1) // PAGE * PAGE
     return off, raw, stride
 
 
-def make_shape(d_model, n_experts, top_k, d_ff, group_size=64, norm_topk=True, bits=4):
-    return SmoeMoeShape(d_model, n_experts, top_k, d_ff, group_size, bits, 1 if norm_topk else 0)
+def make_shape(d_model, n_experts, top_k, d_ff, group_size=64, norm_topk=True, bits=4, quant=QUANT_SMOEQ4):
+    return SmoeMoeShape(d_model, n_experts, top_k, d_ff, group_size, bits, 1 if norm_topk else 0, quant)
 
 
 def make_layer(norm_w: int, router_w: int, experts: int, stride: int, off):
@@ -214,7 +224,7 @@ class Context:
     def _check(self, rc, what):
         if rc != SMOE_OK:
             msg = self.lib.smoe_hip_last_error(self.ptr)
-            raise SmoeError(f"{what}: {_ERR_NAMES.get(rc, rc)} {msg.decode() if msg else ''}")
+            raise SmoeError(f"{what}: {_ERR_NAMES.get(rc, rc)} {msg.decode() if msg else ''}", rc)
 
     # -- stream -------------------------------------------------------------
     def set_stream(self, stream_handle: int | None):
@@ -316,6 +326,10 @@ class Context:
     # -- synthetic inputs -----------------------------------------------------
     def quantize_q4(self, w: int, n: int, group: int, packed: int, scales: int):
         self._check(self.lib.smoe_hip_quantize_q4(self.ptr, w, n, group, packed, scales), "quantize_q4")
+
+    def quantize_q4_scale_min(self, w: int, n: int, group: int, packed: int, scales: int, mins: int):
+        self._check(self.lib.smoe_hip_quantize_q4_scale_min(self.ptr, w, n, group, packed, scales, mins),
+                    "quantize_q4_scale_min")
 
     def synth_normal(self, out: int, n: int, seed: int, stream: int, stddev: float):
         self._check(self.lib.smoe_hip_synth_normal(self.ptr, out, n, seed, stream, stddev), "synth_normal")

@@ -39,10 +39,10 @@ class Layer:
     """One MoE layer of a given shape, resident on cuda:0, plus host copies."""
 
     def __init__(self, ctx, D, E, K, I, layer_id=0, seed=SEED, norm_topk=True, router_std=0.02,
-                 host=True):
-        self.D, self.E, self.K, self.I = D, E, K, I
-        self.shape = smoe_amd.make_shape(D, E, K, I, 64, norm_topk)
-        self.off, self.raw, self.stride = smoe_amd.blob_layout(D, I)
+                 host=True, quant=0):
+        self.D, self.E, self.K, self.I, self.quant = D, E, K, I, quant
+        self.shape = smoe_amd.make_shape(D, E, K, I, 64, norm_topk, quant=quant)
+        self.off, self.raw, self.stride = smoe_amd.blob_layout(D, I, quant=quant)
         dev = torch.device("cuda", 0)
         self.pool = torch.zeros(E * self.stride, dtype=torch.uint8, device=dev)
         ctx.synth_expert_pool(self.pool.data_ptr(), layer_id, 1, E, self.stride, self.shape, seed, 0.02)
@@ -64,7 +64,7 @@ class Layer:
 
     def oracle_shape(self):
         return dict(d_model=self.D, n_experts=self.E, top_k=self.K, d_ff=self.I, group_size=64,
-                    norm_topk=self.shape.norm_topk)
+                    norm_topk=self.shape.norm_topk, quant=self.quant)
 
     def oracle_decode(self, oracle, hidden):
         return oracle.moe_decode_layer(self.oracle_shape(), self.h_norm, self.h_router, self.h_pool,
@@ -81,14 +81,22 @@ def hidden_states(ctx, T, D, index0=0, seed=SEED):
 def q4_matrix_f64(layer, e, k):
     """Matrix k (0 gate [I x D], 1 up [I x D], 2 down [D x I]) of expert e,
     dequantised in fp64: (c - 7.5) / 7.5 * scale per 64-group, low nibble
-    first (shatter_moe.py:371-387)."""
+    first (shatter_moe.py:371-387); for the scale+min format c * s + m with
+    the bf16 scales and the mins after them."""
     blob = layer.h_pool[e * layer.stride:(e + 1) * layer.stride]
     n = layer.D * layer.I
     pk = blob[layer.off[2 * k]:layer.off[2 * k] + n // 2]
-    sc = blob[layer.off[2 * k + 1]:layer.off[2 * k + 1] + 2 * (n // 64)].view(np.float16).astype(np.float64)
     codes = np.empty(n, np.float64)
     codes[0::2] = pk & 15
     codes[1::2] = pk >> 4
+    if getattr(layer, "quant", 0):
+        so = layer.off[2 * k + 1]
+        bf = lambda a: (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        sc = bf(blob[so:so + 2 * (n // 64)].view(np.uint16))
+        mn = bf(blob[so + 2 * (n // 64):so + 4 * (n // 64)].view(np.uint16))
+        w = codes * np.repeat(sc, 64) + np.repeat(mn, 64)
+        return w.reshape((layer.I, layer.D) if k < 2 else (layer.D, layer.I))
+    sc = blob[layer.off[2 * k + 1]:layer.off[2 * k + 1] + 2 * (n // 64)].view(np.float16).astype(np.float64)
     w = (codes - 7.5) / 7.5 * np.repeat(sc, 64)
     return w.reshape((layer.I, layer.D) if k < 2 else (layer.D, layer.I))
 

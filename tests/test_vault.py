@@ -35,7 +35,7 @@ def patch(path, offset, fmt, value):
 def expect_error(path, code, text):
     with pytest.raises(smoe_amd.SmoeError) as ei:
         smoe_amd.Vault(path)
-    assert ei.value.args[1] == code, ei.value
+    assert ei.value.code == code, ei.value
     assert text in str(ei.value), ei.value
 
 
@@ -188,4 +188,4 @@ def test_load_rejects_a_small_pool(tmp_path):
     v = smoe_amd.Vault(write(tmp_path))
     with pytest.raises(smoe_amd.SmoeError) as ei:
         v.load(1 << 40, v.pool_bytes - 1)
-    assert ei.value.args[1] == smoe_amd.SMOE_ERR_CAPACITY
+    assert ei.value.code == smoe_amd.SMOE_ERR_CAPACITY
