@@ -458,7 +458,12 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
         if constexpr (CHAIN && CPL == 1)
             if (io.next_router && producer) {
                 const uint32_t r = (lane >> 5) && second ? t + nbx : t;
-                touch = io.next_router[static_cast<size_t>(r) * D + min((static_cast<uint32_t>(lane) & 31u) * 64u, D - 1)];
+                // (a global, not a flat, load: a flat load in flight leaves the
+                // compiler unable to count the loads before it, and every later
+                // wait then drains all of them -- the gate/up dots would wait
+                // for the last row instead of starting as the first rows land)
+                touch = *gptr(io.next_router + static_cast<size_t>(r) * D +
+                              min((static_cast<uint32_t>(lane) & 31u) * 64u, D - 1));
             }
         // the rest of the top-k while the rows land
         topk_net_finish<VPL>(v, d.E, d.K, d.norm_topk, my_id, my_w, slots, net);
@@ -471,15 +476,24 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
             if constexpr (DFIRST)
                 if (t < n_down) issue_down(blob);
             if (t < n_up) issue_up(blob);
+            // (rare: the new rows land before the dots start, so the rows of
+            // the usual path keep counted waits, row by row as they land)
+            vm_wait_all();
         }
     } else {
         expert = prop;
         blob = L.experts + static_cast<size_t>(prop) * L.stride;
     }
-    if (x == 0 && t == 0 && static_cast<uint32_t>(lane) < d.K) {
-        ids_out[lane] = my_id;
-        w_out[lane] = my_w;
-    }
+    // (the routing outputs are stored at the end of the layer: a store here,
+    // in one wave's branch, would leave the loads in flight uncounted, and
+    // the compiler drains the wave's memory operations before it anywhere
+    // earlier)
+    auto store_routing = [&] {
+        if (x == 0 && t == 0 && static_cast<uint32_t>(lane) < d.K) {
+            ids_out[lane] = my_id;
+            w_out[lane] = my_w;
+        }
+    };
 
     // 3. gate/up rows of rank x -> h
     if (t < n_up) {
@@ -695,6 +709,7 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
             }
         }
     }
+    store_routing();
     if (timed_out && io.abort && lane == 0)
         __hip_atomic_store(io.abort, io.abort_val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // (keeps the touch's register until every load of the layer has landed)
