@@ -81,11 +81,17 @@ __device__ __forceinline__ uint32_t get_agent32(const uint32_t* p)
 {
     return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// drop this CU's L1 lines (data other CUs of the XCD rewrote in the L2
-// since they were read is then read from the L2)
-__device__ __forceinline__ void l1_invalidate()
+// 16 bytes that other CUs wrote during the launch: two agent-scope loads,
+// which read the L2 past this CU's L1 (a plain load can hit a line the L1
+// still holds from before the write: a workgroup-scope invalidate does not
+// drop it, and the agent-scope one drops the CU's whole L1 at a cost of
+// microseconds)
+__device__ __forceinline__ float4 load_f4_agent(const float* p)
 {
-    asm volatile("buffer_inv sc0" ::: "memory");
+    const uint64_t a = get_agent(reinterpret_cast<const uint64_t*>(p));
+    const uint64_t b = get_agent(reinterpret_cast<const uint64_t*>(p) + 1);
+    return make_float4(__uint_as_float(static_cast<uint32_t>(a)), __uint_as_float(static_cast<uint32_t>(a >> 32)),
+                       __uint_as_float(static_cast<uint32_t>(b)), __uint_as_float(static_cast<uint32_t>(b >> 32)));
 }
 __device__ __forceinline__ void vm_wait_all()
 {
@@ -168,20 +174,22 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
     constexpr uint32_t QS = CPL * WAVE + 1;
     __shared__ float4 hid_s[NW > 1 ? 8 * QS : 1];
     __shared__ uint4 nrm_s[NW > 1 ? 4 * QS : 1];
-    auto load_hidden = [&] {
+    // (coherent: the input was written by other CUs during the launch)
+    auto load_hidden = [&](bool coherent) {
+        auto ld = [&](const float* p) { return coherent ? load_f4_agent(p) : load_f4(p); };
         if constexpr (NW > 1) {
             for (uint32_t f = threadIdx.x; f < D / 4; f += NW * WAVE)
-                hid_s[(f & 7u) * QS + (f >> 3)] = load_f4(io.hin + 4 * f);
+                hid_s[(f & 7u) * QS + (f >> 3)] = ld(io.hin + 4 * f);
         } else {
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 const uint32_t c = min(lane + WAVE * j, nch - 1);
 #pragma unroll
-                for (int q = 0; q < 8; ++q) xv[j][q] = load_f4(io.hin + c * 32 + q * 4);
+                for (int q = 0; q < 8; ++q) xv[j][q] = ld(io.hin + c * 32 + q * 4);
             }
         }
     };
-    if (!io.wait) load_hidden();
+    if (!io.wait) load_hidden(false);
     if constexpr (NW > 1) {
         for (uint32_t f = threadIdx.x; f < D / 8; f += NW * WAVE)
             nrm_s[(f & 3u) * QS + (f >> 2)] = load_u4(L.norm_w + 8 * f);
@@ -231,8 +239,7 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
             } while (!all);
         }
         if constexpr (NW > 1) __syncthreads();
-        l1_invalidate();
-        load_hidden();
+        load_hidden(true);
     }
     if constexpr (NW > 1) {
         __syncthreads();
