@@ -944,28 +944,47 @@ def grouped_traffic(workload, symbol):
 def rocprof_summary(d, config, pmc_out, copy_mib, workload="decode"):
     """Print a per-kernel summary of a rocprofv3 output directory: kernel
     stats (--kernel-trace --stats) and, for --pmc runs, the average counter
-    value per dispatch of each kernel.  With --pmc-out (and the size given by
-    --calibrate-copy-mib), FETCH_SIZE/WRITE_SIZE averages of the decode kernels
-    are scaled by expected/measured of the same counter for the calibration
-    kernel (b = -a over that many MiB: reads and writes exactly that much) and
-    merged into that JSON file."""
+    value per dispatch of each kernel.  A kernel's full-size dispatches (at
+    least half its largest) are also summarised apart: the parity leg runs the
+    decode kernel on one layer at a time beside the whole-step launches.  With
+    --pmc-out (and the size given by --calibrate-copy-mib), FETCH_SIZE/WRITE_SIZE
+    of the decode kernels' full-size dispatches are scaled by expected/measured
+    of the same counter for the calibration kernel (b = -a over that many MiB:
+    reads and writes exactly that much) and merged into that JSON file."""
     for p in sorted(glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)):
         print(f"== {os.path.basename(p)}")
         print(f"{'calls':>7} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'pct':>6}  kernel")
         for r in csv.DictReader(open(p)):
             print(f"{int(r['Calls']):7d} {float(r['AverageNs']) / 1e3:9.3f} {float(r['MinNs']) / 1e3:9.3f} "
                   f"{float(r['MaxNs']) / 1e3:9.3f} {float(r['Percentage']):6.2f}  {r['Name'][:90]}")
-    acc = {}
+    for p in sorted(glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)):
+        durs = {}
+        for r in csv.DictReader(open(p)):
+            durs.setdefault(r["Kernel_Name"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        print(f"== {os.path.basename(p)}: full-size dispatches (at least half the kernel's longest)")
+        print(f"{'calls':>7} {'avg_us':>9} {'min_us':>9} {'max_us':>9} {'of':>6}  kernel")
+        for k, v in sorted(durs.items(), key=lambda kv: -sum(kv[1])):
+            big = [x for x in v if x >= 0.5 * max(v)]
+            print(f"{len(big):7d} {sum(big) / len(big):9.3f} {min(big):9.3f} {max(big):9.3f} {len(v):6d}  {k[:90]}")
+    per = {}
     for p in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
         for r in csv.DictReader(open(p)):
-            s = acc.setdefault((r["Kernel_Name"], r["Counter_Name"]), [0.0, 0])
-            s[0] += float(r["Counter_Value"])
-            s[1] += 1
-    if not acc:
+            key = (r["Kernel_Name"], r["Counter_Name"])
+            disp = r.get("Dispatch_Id") or r.get("Correlation_Id") or str(len(per.get(key, {})))
+            per.setdefault(key, {})
+            per[key][disp] = per[key].get(disp, 0.0) + float(r["Counter_Value"])
+    if not per:
         return
-    print("== counters (average per dispatch)")
+    acc, full = {}, {}
+    for key, dv in per.items():
+        v = list(dv.values())
+        acc[key] = (sum(v), len(v))
+        big = [x for x in v if x >= 0.5 * max(v)]
+        full[key] = (sum(big), len(big))
+    print("== counters (average per dispatch; full-size dispatches: at least half the largest)")
     for (k, cn), (tot, n) in sorted(acc.items()):
-        print(f"{cn:>12} {tot / n:14.1f}  n={n:5d}  {k[:90]}")
+        ft, fn = full[(k, cn)]
+        print(f"{cn:>12} {tot / n:14.1f}  n={n:5d}  full-size {ft / fn:14.1f}  n={fn:5d}  {k[:80]}")
     if not (pmc_out and copy_mib):
         return
     data = json.load(open(pmc_out)) if os.path.exists(pmc_out) else {}
@@ -984,7 +1003,7 @@ def rocprof_summary(d, config, pmc_out, copy_mib, workload="decode"):
         data.setdefault("_calibration", {})[cn] = {"copy_mib": copy_mib, "copy_kib_measured": round(copy_kib, 1),
                                                     "scale": round(scale, 4)}
         for sym in symbols:
-            vals = [tot / n for (k, c2), (tot, n) in acc.items() if c2 == cn and sym in k]
+            vals = [tot / n for (k, c2), (tot, n) in full.items() if c2 == cn and sym in k]
             if vals:
                 e = ent.setdefault(sym, {})
                 e[cn + "_kib"] = round(vals[0], 1)
