@@ -706,8 +706,16 @@ __device__ __forceinline__ bool moe_layer_step(const MoeDims& d, const LayerDesc
 #pragma unroll
                 for (int r = 0; r < 8; ++r) sum = fmaf(readlane_f32(my_w, r), y[r], sum);
                 // (the input as this wave read it at the start of the layer: no
-                // other wave writes these rows before this one)
-                io.hout[row] = io.hin[row] + sum;
+                // other wave writes these rows before this one; blocks of
+                // shared loads hold it in LDS)
+                float hin_row;
+                if constexpr (NW > 1) {
+                    const uint32_t f = row >> 2;
+                    hin_row = reinterpret_cast<const float*>(hid_s)[((f & 7u) * QS + (f >> 3)) * 4u + (row & 3u)];
+                } else {
+                    hin_row = io.hin[row];
+                }
+                io.hout[row] = hin_row + sum;
             }
             if (io.flag) {
                 // the rows are in the L2 before the flag says so
